@@ -1,0 +1,397 @@
+// Dynamic and static e4m3fn quantisation (contracts Q-A, Q-W, G).
+//
+// Row mode keeps one row per wavefront in registers: one HBM read of the bf16
+// row, a 64-lane max reduction, then the codes are produced from registers
+// (3 bytes of HBM traffic per element).  Tensor mode writes per-workgroup
+// partial maxima in a first launch and every workgroup of the second launch
+// re-reduces those partials (at most 1024 floats) before quantising, so no
+// atomics and no memset are needed.
+//
+// Bit-exactness: x/s is an IEEE division (never x * (1/s)); the fp32 ->
+// e4m3fn conversion is v_cvt_pk_fp8_f32 after clamping to +-448.
+#pragma clang fp contract(off)
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;            // wavefronts per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxPartials = 1024;   // tensor-mode partial maxima
+
+template <bool GELU>
+FVSR_DEV float load_val(const uint16_t* p) {
+  float v = bf2f(*p);
+  return GELU ? gelu_tanh_bf16(v) : v;
+}
+
+// Apply GELU to a packed chunk of 8 bf16 (the result is bf16-valued, so it is
+// stored back packed).
+FVSR_DEV u32x4_t gelu_chunk(u32x4_t c) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = pack_bf16x2(gelu_tanh_bf16(bf_lo(c[i])), gelu_tanh_bf16(bf_hi(c[i])));
+  return r;
+}
+
+FVSR_DEV float chunk_absmax(u32x4_t c) {
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) m = fmaxf(m, fmaxf(fabsf(bf_lo(c[i])), fabsf(bf_hi(c[i]))));
+  return m;
+}
+
+FVSR_DEV u32x2_t chunk_codes(u32x4_t c, float s) {
+  u32x2_t r;
+  r[0] = pack_e4m3x4(clamp448(bf_lo(c[0]) / s), clamp448(bf_hi(c[0]) / s),
+                     clamp448(bf_lo(c[1]) / s), clamp448(bf_hi(c[1]) / s));
+  r[1] = pack_e4m3x4(clamp448(bf_lo(c[2]) / s), clamp448(bf_hi(c[2]) / s),
+                     clamp448(bf_lo(c[3]) / s), clamp448(bf_hi(c[3]) / s));
+  return r;
+}
+
+FVSR_DEV float qscale(float amax) { return fmaxf(amax, 1e-12f) / 448.0f; }
+
+// ---------------------------------------------------------------------------
+// Row mode, register resident: cols % 8 == 0, cols <= 512*VPL, 16-byte rows.
+// ---------------------------------------------------------------------------
+template <int VPL, bool GELU>
+__global__ __launch_bounds__(kThreads) void quant_rows_vec(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ld;
+  const int64_t nchunk = cols >> 3;
+  u32x4_t v[VPL];
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < nchunk) {
+      v[j] = *(const u32x4_t*)(xr + c * 8);
+      if (GELU) v[j] = gelu_chunk(v[j]);
+      m = fmaxf(m, chunk_absmax(v[j]));
+    }
+  }
+  const float amax = wave_max(m);
+  const float s = qscale(amax);
+  uint8_t* qr = codes + row * cols;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < nchunk) *(u32x2_t*)(qr + c * 8) = chunk_codes(v[j], s);
+  }
+  if (lane == 0) scale_out[row] = amax / 448.0f;
+}
+
+// Row mode, any shape: two passes over the row (the second hits L2).
+template <bool GELU>
+__global__ __launch_bounds__(kThreads) void quant_rows_generic(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * ld;
+  float m = 0.0f;
+  for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(xr + c)));
+  const float amax = wave_max(m);
+  const float s = qscale(amax);
+  uint8_t* qr = codes + row * cols;
+  for (int64_t c = lane; c < cols; c += 64) {
+    float q = clamp448(load_val<GELU>(xr + c) / s);
+    qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
+  }
+  if (lane == 0) scale_out[row] = amax / 448.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Tensor mode.
+// ---------------------------------------------------------------------------
+FVSR_DEV float block_max(float m, float* red) {
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) r = fmaxf(r, red[w]);
+  return r;
+}
+
+// Partial |x| maxima: workgroup b covers rows b, b+G, ... (one wave per row).
+template <bool GELU, bool VEC>
+__global__ __launch_bounds__(kThreads) void amax_partial(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    float* __restrict__ part) {
+  __shared__ float red[kWaves];
+  const int lane = threadIdx.x & 63;
+  float m = 0.0f;
+  for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * kWaves) {
+    const uint16_t* xr = x + row * ld;
+    if (VEC) {
+      for (int64_t c = lane; c < (cols >> 3); c += 64) {
+        u32x4_t v = *(const u32x4_t*)(xr + c * 8);
+        if (GELU) v = gelu_chunk(v);
+        m = fmaxf(m, chunk_absmax(v));
+      }
+    } else {
+      for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(xr + c)));
+    }
+  }
+  m = block_max(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+// Max of n floats -> part[blockIdx.x] (used on GEMM-epilogue partial maxima).
+__global__ __launch_bounds__(kThreads) void max_reduce(const float* __restrict__ in, int64_t n,
+                                                       float* __restrict__ part) {
+  __shared__ float red[kWaves];
+  float m = 0.0f;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * kThreads)
+    m = fmaxf(m, in[i]);
+  m = block_max(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
+}
+
+FVSR_DEV float reduce_partials(const float* __restrict__ part, int nparts, float* red) {
+  float m = 0.0f;
+  for (int i = threadIdx.x; i < nparts; i += kThreads) m = fmaxf(m, part[i]);
+  return block_max(m, red);
+}
+
+template <bool GELU, bool VEC>
+__global__ __launch_bounds__(kThreads) void quant_tensor(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    const float* __restrict__ part, int nparts, uint8_t* __restrict__ codes,
+    float* __restrict__ scale_out) {
+  __shared__ float red[kWaves];
+  const float amax = reduce_partials(part, nparts, red);
+  const float s = qscale(amax);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = amax / 448.0f;
+  const int lane = threadIdx.x & 63;
+  for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * kWaves) {
+    const uint16_t* xr = x + row * ld;
+    uint8_t* qr = codes + row * cols;
+    if (VEC) {
+      for (int64_t c = lane; c < (cols >> 3); c += 64) {
+        u32x4_t v = *(const u32x4_t*)(xr + c * 8);
+        if (GELU) v = gelu_chunk(v);
+        *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s);
+      }
+    } else {
+      for (int64_t c = lane; c < cols; c += 64) {
+        float q = clamp448(load_val<GELU>(xr + c) / s);
+        qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
+      }
+    }
+  }
+}
+
+// Row mode with the row amax given as nparts partial maxima per row.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void quant_rows_from_amax(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, const float* __restrict__ apart,
+    int64_t nparts, uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  float m = 0.0f;
+  for (int64_t i = lane; i < nparts; i += 64) m = fmaxf(m, apart[row * nparts + i]);
+  const float amax = wave_max(m);
+  const float s = qscale(amax);
+  const uint16_t* xr = x + row * cols;
+  uint8_t* qr = codes + row * cols;
+  if (VEC) {
+    for (int64_t c = lane; c < (cols >> 3); c += 64) {
+      u32x4_t v = *(const u32x4_t*)(xr + c * 8);
+      *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s);
+    }
+  } else {
+    for (int64_t c = lane; c < cols; c += 64) {
+      float q = clamp448(bf2f(xr[c]) / s);
+      qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
+    }
+  }
+  if (lane == 0) scale_out[row] = amax / 448.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Static weight quantisation (fp8_linear.py:17-22 and its per-channel form).
+// ---------------------------------------------------------------------------
+FVSR_DEV float weight_scale(float amax) {
+  const float lo = round_bf16(1e-12f);
+  float s = round_bf16(amax / 448.0f);
+  return fmaxf(s, lo);
+}
+
+FVSR_DEV uint8_t weight_code(float w, float s, bool per_channel) {
+  float v = w / s;
+  if (!per_channel) v = round_bf16(v);
+  v = clamp448(v);  // |v| <= 450 after rounding; 450 -> 448 either way
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xff);
+}
+
+__global__ __launch_bounds__(kThreads) void quant_weight_rows(
+    const uint16_t* __restrict__ w, int64_t n, int64_t k, uint8_t* __restrict__ codes,
+    float* __restrict__ scale_out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= n) return;
+  const uint16_t* wr = w + row * k;
+  float m = 0.0f;
+  for (int64_t c = lane; c < k; c += 64) m = fmaxf(m, fabsf(bf2f(wr[c])));
+  const float s = weight_scale(wave_max(m));
+  for (int64_t c = lane; c < k; c += 64) codes[row * k + c] = weight_code(bf2f(wr[c]), s, true);
+  if (lane == 0) scale_out[row] = s;
+}
+
+__global__ __launch_bounds__(kThreads) void quant_weight_tensor(
+    const uint16_t* __restrict__ w, int64_t n, int64_t k, const float* __restrict__ part,
+    int nparts, uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
+  __shared__ float red[kWaves];
+  const float s = weight_scale(reduce_partials(part, nparts, red));
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
+  const int64_t total = n * k;
+  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * kThreads)
+    codes[i] = weight_code(bf2f(w[i]), s, false);
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+int partial_blocks(int64_t rows) {
+  int64_t b = (rows + kWaves - 1) / kWaves;
+  return (int)(b < kMaxPartials ? (b > 0 ? b : 1) : kMaxPartials);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <bool GELU>
+int launch_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8_t* q,
+                float* s, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
+  const bool vec = (cols % 8 == 0) && (ld % 8 == 0) && aligned16(x) && aligned16(q);
+  const int64_t vpl = (cols / 8 + 63) / 64;
+  if (vec && vpl <= 3) {
+    hipLaunchKernelGGL((quant_rows_vec<3, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
+  } else if (vec && vpl <= 6) {
+    hipLaunchKernelGGL((quant_rows_vec<6, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
+  } else if (vec && vpl <= 18) {
+    hipLaunchKernelGGL((quant_rows_vec<18, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
+  } else {
+    hipLaunchKernelGGL((quant_rows_generic<GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
+  }
+  return fvsr_launch_status();
+}
+
+template <bool GELU>
+int launch_tensor(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8_t* q,
+                  float* s, float* ws, hipStream_t st) {
+  const int P = partial_blocks(rows);
+  const bool vec = (cols % 8 == 0) && (ld % 8 == 0) && aligned16(x) && aligned16(q);
+  if (vec) {
+    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
+                       ld, ws);
+    hipLaunchKernelGGL((quant_tensor<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
+                       ld, ws, P, q, s);
+  } else {
+    hipLaunchKernelGGL((amax_partial<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, rows,
+                       cols, ld, ws);
+    hipLaunchKernelGGL((quant_tensor<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, rows,
+                       cols, ld, ws, P, q, s);
+  }
+  return fvsr_launch_status();
+}
+
+}  // namespace
+
+extern "C" int64_t fvsr_quant_workspace_floats(int64_t rows, int64_t cols, int mode) {
+  (void)cols;
+  (void)mode;
+  return partial_blocks(rows);
+}
+
+extern "C" int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mode,
+                              int gelu, void* codes, float* scale_out, float* workspace,
+                              int64_t workspace_floats, void* stream) {
+  if (rows < 0 || cols < 0 || ld < cols || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW))
+    return FVSR_EINVAL;
+  if (rows == 0 || cols == 0) return FVSR_OK;
+  if (!x || !codes || !scale_out) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint8_t* qp = (uint8_t*)codes;
+  if (mode == FVSR_SCALE_ROW)
+    return gelu ? launch_rows<true>(xp, rows, cols, ld, qp, scale_out, st)
+                : launch_rows<false>(xp, rows, cols, ld, qp, scale_out, st);
+  if (!workspace || workspace_floats < partial_blocks(rows)) return FVSR_EWORKSPACE;
+  return gelu ? launch_tensor<true>(xp, rows, cols, ld, qp, scale_out, workspace, st)
+              : launch_tensor<false>(xp, rows, cols, ld, qp, scale_out, workspace, st);
+}
+
+extern "C" int fvsr_quant_fp8_from_amax(const void* x, int64_t rows, int64_t cols,
+                                        const float* amax_part, int64_t nparts, int mode,
+                                        void* codes, float* scale_out, float* workspace,
+                                        int64_t workspace_floats, void* stream) {
+  if (rows < 0 || cols < 0 || nparts <= 0 ||
+      (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW))
+    return FVSR_EINVAL;
+  if (rows == 0 || cols == 0) return FVSR_OK;
+  if (!x || !codes || !scale_out || !amax_part) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint8_t* qp = (uint8_t*)codes;
+  const bool vec = (cols % 8 == 0) && aligned16(x) && aligned16(codes);
+  if (mode == FVSR_SCALE_ROW) {
+    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
+    if (vec)
+      hipLaunchKernelGGL((quant_rows_from_amax<true>), grid, block, 0, st, xp, rows, cols,
+                         amax_part, nparts, qp, scale_out);
+    else
+      hipLaunchKernelGGL((quant_rows_from_amax<false>), grid, block, 0, st, xp, rows, cols,
+                         amax_part, nparts, qp, scale_out);
+    return fvsr_launch_status();
+  }
+  const int P = partial_blocks(rows);
+  if (!workspace || workspace_floats < P) return FVSR_EWORKSPACE;
+  hipLaunchKernelGGL(max_reduce, dim3(P), dim3(kThreads), 0, st, amax_part, rows * nparts,
+                     workspace);
+  if (vec)
+    hipLaunchKernelGGL((quant_tensor<false, true>), dim3(P), dim3(kThreads), 0, st, xp, rows,
+                       cols, cols, workspace, P, qp, scale_out);
+  else
+    hipLaunchKernelGGL((quant_tensor<false, false>), dim3(P), dim3(kThreads), 0, st, xp, rows,
+                       cols, cols, workspace, P, qp, scale_out);
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_quant_weight_fp8(const void* w, int64_t n, int64_t k, int mode, void* codes,
+                                     float* scale_out, float* workspace, int64_t workspace_floats,
+                                     void* stream) {
+  if (n < 0 || k < 0 || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW)) return FVSR_EINVAL;
+  if (n == 0 || k == 0) return FVSR_OK;
+  if (!w || !codes || !scale_out) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* wp = (const uint16_t*)w;
+  uint8_t* qp = (uint8_t*)codes;
+  if (mode == FVSR_SCALE_ROW) {
+    hipLaunchKernelGGL(quant_weight_rows, dim3((unsigned)((n + kWaves - 1) / kWaves)),
+                       dim3(kThreads), 0, st, wp, n, k, qp, scale_out);
+    return fvsr_launch_status();
+  }
+  const int P = partial_blocks(n);
+  if (!workspace || workspace_floats < P) return FVSR_EWORKSPACE;
+  hipLaunchKernelGGL((amax_partial<false, false>), dim3(P), dim3(kThreads), 0, st, wp, n, k, k,
+                     workspace);
+  hipLaunchKernelGGL(quant_weight_tensor, dim3(P), dim3(kThreads), 0, st, wp, n, k, workspace, P,
+                     qp, scale_out);
+  return fvsr_launch_status();
+}
+
+extern "C" const char* fvsr_version(void) { return "fvsr 0.1.0 gfx950"; }

@@ -1,0 +1,171 @@
+// RMSNorm over the full hidden dim + interleaved RoPE per head (contract R),
+// bandwidth bound.
+//
+// One wavefront per row.  Each lane holds 8 contiguous elements per chunk, so
+// a RoPE pair (2i, 2i+1) is always inside one lane's registers and the partner
+// swap costs nothing.  The (cos, sin) table is read in its interleaved
+// [L, head_dim/2, 2] fp32 layout — the view_as_real of the complex freqs_cis —
+// as two 16-byte loads per chunk.
+#include "common.h"
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+
+template <int VPL, bool ROPE>
+FVSR_DEV void rms_rope_row(const uint16_t* xr, const uint16_t* __restrict__ w,
+                           const float* __restrict__ cs_row, uint16_t* outr,
+                           int64_t D, int64_t head_dim, float eps, int lane) {
+  const int64_t nchunk = D >> 3;
+  u32x4_t v[VPL];
+  float sq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < nchunk) {
+      v[j] = *(const u32x4_t*)(xr + c * 8);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float a = bf_lo(v[j][i]), b = bf_hi(v[j][i]);
+        sq += a * a + b * b;
+      }
+    }
+  }
+  const float r = rsqrtf(wave_sum(sq) / (float)D + eps);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t c = lane + 64 * j;
+    if (c < nchunk) {
+      const u32x4_t wv = *(const u32x4_t*)(w + c * 8);
+      u32x4_t o;
+      f32x4_t cs0, cs1;
+      if (ROPE) {
+        const int64_t i0 = ((c * 8) % head_dim) >> 1;  // first pair index of this chunk
+        cs0 = *(const f32x4_t*)(cs_row + 2 * i0);       // c0 s0 c1 s1
+        cs1 = *(const f32x4_t*)(cs_row + 2 * i0 + 4);   // c2 s2 c3 s3
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ye = round_bf16(bf_lo(v[j][i]) * r) * bf_lo(wv[i]);
+        const float yo = round_bf16(bf_hi(v[j][i]) * r) * bf_hi(wv[i]);
+        if (ROPE) {
+          const float cc = i < 2 ? cs0[2 * i] : cs1[2 * (i - 2)];
+          const float ss = i < 2 ? cs0[2 * i + 1] : cs1[2 * (i - 2) + 1];
+          o[i] = pack_bf16x2(ye * cc - yo * ss, ye * ss + yo * cc);
+        } else {
+          o[i] = pack_bf16x2(ye, yo);
+        }
+      }
+      *(u32x4_t*)(outr + c * 8) = o;
+    }
+  }
+}
+
+template <int VPL, bool ROPE>
+__global__ __launch_bounds__(kThreads) void rms_rope_vec(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ cs,
+    uint16_t* __restrict__ out, int64_t rows, int64_t L, int64_t D, int64_t head_dim, float eps) {
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  rms_rope_row<VPL, ROPE>(x + row * D, w, ROPE ? cs + (row % L) * head_dim : nullptr,
+                          out + row * D, D, head_dim, eps, threadIdx.x & 63);
+}
+
+// q and k rows in one grid: blockIdx.y selects the tensor.
+// Row strides ld_in / ld_out let q and k be column slices of a fused QKV
+// projection output and be normalised in place (each wave reads its whole row
+// into registers before it writes).
+template <int VPL>
+__global__ __launch_bounds__(kThreads) void rms_rope_qk_vec(
+    const uint16_t* q, const uint16_t* k, const uint16_t* __restrict__ wq,
+    const uint16_t* __restrict__ wk, const float* __restrict__ cs, uint16_t* oq, uint16_t* ok,
+    int64_t rows, int64_t L, int64_t D, int64_t head_dim, float eps, int64_t ld_in,
+    int64_t ld_out) {
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bool isk = blockIdx.y != 0;
+  rms_rope_row<VPL, true>((isk ? k : q) + row * ld_in, isk ? wk : wq, cs + (row % L) * head_dim,
+                          (isk ? ok : oq) + row * ld_out, D, head_dim, eps, threadIdx.x & 63);
+}
+
+// Any shape: scalar loads, partner element read directly.
+__global__ __launch_bounds__(kThreads) void rms_rope_generic(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ cs,
+    uint16_t* __restrict__ out, int64_t rows, int64_t L, int64_t D, int64_t head_dim, float eps,
+    int rope) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * D;
+  float sq = 0.0f;
+  for (int64_t d = lane; d < D; d += 64) {
+    const float a = bf2f(xr[d]);
+    sq += a * a;
+  }
+  const float r = rsqrtf(wave_sum(sq) / (float)D + eps);
+  const int64_t s = row % L;
+  for (int64_t d = lane; d < D; d += 64) {
+    const float y = round_bf16(bf2f(xr[d]) * r) * bf2f(w[d]);
+    float o = y;
+    if (rope) {
+      const int64_t dp = d ^ 1;
+      const float yp = round_bf16(bf2f(xr[dp]) * r) * bf2f(w[dp]);
+      const int64_t i = (d % head_dim) >> 1;
+      const float cc = cs[(s * (head_dim >> 1) + i) * 2], ss = cs[(s * (head_dim >> 1) + i) * 2 + 1];
+      o = (d & 1) ? (yp * ss + y * cc) : (y * cc - yp * ss);
+    }
+    out[row * D + d] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffff);
+  }
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace
+
+extern "C" int fvsr_rms_rope(const void* x, const void* weight, const float* cs, void* out,
+                             int64_t B, int64_t L, int64_t D, int64_t head_dim, float eps,
+                             int rope, void* stream) {
+  if (B < 0 || L < 0 || D <= 0) return FVSR_EINVAL;
+  if (rope && (head_dim <= 0 || head_dim % 2 || D % head_dim || !cs)) return FVSR_EINVAL;
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!x || !weight || !out) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
+  const uint16_t *xp = (const uint16_t*)x, *wp = (const uint16_t*)weight;
+  uint16_t* op = (uint16_t*)out;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(weight) &&
+                   aligned16(out) && (!rope || (head_dim % 8 == 0 && aligned16(cs)));
+  if (vec && rope)
+    hipLaunchKernelGGL((rms_rope_vec<3, true>), grid, block, 0, st, xp, wp, cs, op, rows, L, D,
+                       head_dim, eps);
+  else if (vec)
+    hipLaunchKernelGGL((rms_rope_vec<3, false>), grid, block, 0, st, xp, wp, cs, op, rows, L, D,
+                       head_dim > 0 ? head_dim : D, eps);
+  else
+    hipLaunchKernelGGL(rms_rope_generic, grid, block, 0, st, xp, wp, cs, op, rows, L, D,
+                       head_dim > 0 ? head_dim : D, eps, rope);
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_rms_rope_qk(const void* q, const void* k, const void* wq, const void* wk,
+                                const float* cs, void* out_q, void* out_k, int64_t B, int64_t L,
+                                int64_t D, int64_t head_dim, float eps, int64_t ld_in,
+                                int64_t ld_out, void* stream) {
+  if (B < 0 || L < 0 || D <= 0 || head_dim <= 0 || head_dim % 8 || D % head_dim) return FVSR_EINVAL;
+  if (ld_in < D || ld_out < D) return FVSR_EINVAL;
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!q || !k || !wq || !wk || !cs || !out_q || !out_k) return FVSR_EINVAL;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && ld_in % 8 == 0 && ld_out % 8 == 0 &&
+                   aligned16(q) && aligned16(k) && aligned16(wq) && aligned16(wk) &&
+                   aligned16(cs) && aligned16(out_q) && aligned16(out_k);
+  if (!vec) return FVSR_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL((rms_rope_qk_vec<3>), dim3((unsigned)((rows + kWaves - 1) / kWaves), 2),
+                     dim3(kThreads), 0, st, (const uint16_t*)q, (const uint16_t*)k,
+                     (const uint16_t*)wq, (const uint16_t*)wk, cs, (uint16_t*)out_q,
+                     (uint16_t*)out_k, rows, L, D, head_dim, eps, ld_in, ld_out);
+  return fvsr_launch_status();
+}

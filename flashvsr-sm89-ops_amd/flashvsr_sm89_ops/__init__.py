@@ -1,0 +1,44 @@
+"""flashvsr_sm89_ops — the FlashVSR v1.1 Tiny DiT-block operator pack, MI355X
+(gfx950) build.
+
+Same package name, entry point (`enable(pipe)`) and op signatures as
+aireet/flashvsr-sm89-ops; every op runs hand-written HIP kernels from
+libfvsr.so through a C ABI (include/fvsr.h).  Importing the package installs
+the HIP-backed ``block_sparse_attn`` module (see compat_bsa), so import it
+before diffsynth, whose DiT imports block_sparse_attn at module load.
+"""
+from .compat_bsa import active_backend, ensure_bsa_available
+
+ensure_bsa_available()
+
+from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qk  # noqa: E402
+from .fused_adaln import fused_ln_modulate, fused_gate_add, fused_ln_modulate_quant  # noqa: E402
+from .fp8_quant import quantize_fp8, quantize_weight_fp8, FP8_MAX  # noqa: E402
+from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm  # noqa: E402
+from .fp8_ffn import FP8FFN, convert_ffn_fp8, fused_gelu_quant_fp8  # noqa: E402
+from .integrate import enable  # noqa: E402
+from .lcsa import block_sparse_attention, build_csr  # noqa: E402
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "enable",
+    "fused_rms_rope",
+    "fused_rms_rope_qk",
+    "fused_ln_modulate",
+    "fused_ln_modulate_quant",
+    "fused_gate_add",
+    "quantize_fp8",
+    "quantize_weight_fp8",
+    "FP8_MAX",
+    "FP8Linear",
+    "convert_linears_fp8",
+    "fp8_gemm",
+    "FP8FFN",
+    "convert_ffn_fp8",
+    "fused_gelu_quant_fp8",
+    "block_sparse_attention",
+    "build_csr",
+    "active_backend",
+    "ensure_bsa_available",
+]

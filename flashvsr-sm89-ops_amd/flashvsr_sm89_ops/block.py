@@ -1,0 +1,126 @@
+"""The FlashVSR-Tiny DiT block built only from this pack's HIP ops.
+
+This is the unit the rebound ``DiTBlock.forward`` executes per streaming chunk
+(reference integrate.py:151-182 with the self-attention of :47-124), laid out
+for gfx950 instead of as a sequence of eager ops:
+
+  fused_ln_modulate + per-token e4m3 quant     (1 pass, codes only)
+  fused q|k|v projection                       (one FP8 GEMM, N = 3*dim)
+  RMSNorm + RoPE on q and k, in place          (one launch)
+  block-sparse attention                       (window order through token
+                                                maps: no partition copies)
+  per-token quant of the attention output
+  o projection + gate_add                      (FP8 GEMM, gate_add epilogue)
+  fused_ln_modulate + per-token quant
+  ffn.0 + bias + tanh-GELU                     (FP8 GEMM, GELU epilogue + row amax)
+  GELU requant                                 (1 pass)
+  ffn.2 + gate_add                             (FP8 GEMM, gate_add epilogue)
+
+Cross-attention and ``norm3`` are not part of the BASELINE C5 block stack; the
+rebound forward in integrate.py keeps them.  Weights use per-output-channel
+scales, activations per-token scales.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .fp8_ffn import gemm_gelu_quant_fp8
+from .fp8_linear import FP8Linear, fp8_gemm
+from .fp8_quant import quantize_fp8, quantize_weight_fp8
+from .fused_adaln import fused_ln_modulate_quant
+from .fused_rms_rope import fused_rms_rope_qk
+from .lcsa.hip_lcsa import block_sparse_attention_strided
+
+
+def window_token_map(f: int, h: int, w: int, win=(2, 8, 8), device=None) -> torch.Tensor:
+    """int32 [f*h*w]: position in window order -> raster token index, the
+    permutation of WindowPartition3D.partition (lcsa/reference.py:15-21)."""
+    wf, wh, ww = win
+    t = torch.arange(f * h * w, dtype=torch.int32).reshape(f // wf, wf, h // wh, wh, w // ww, ww)
+    t = t.permute(0, 2, 4, 1, 3, 5).reshape(-1)
+    return t.to(device) if device is not None else t
+
+
+class DiTBlockWeights:
+    """FP8 weights of one DiT block: fused qkv [3*dim, dim], o [dim, dim],
+    ffn0 [ffn, dim], ffn2 [dim, ffn] (e4m3 + per-channel fp32 scales, bf16
+    biases), RMSNorm weights and the [6, dim] modulation."""
+
+    def __init__(self, dim: int, ffn_dim: int, device, generator: torch.Generator,
+                 std: float = 0.02):
+        def lin(n, k):
+            w = (torch.randn(n, k, generator=generator) * std).to(torch.bfloat16).to(device)
+            q, s = quantize_weight_fp8(w, per_channel=True)
+            return q, s, torch.zeros(n, dtype=torch.bfloat16, device=device)
+
+        self.qkv = lin(3 * dim, dim)
+        self.o = lin(dim, dim)
+        self.ffn0 = lin(ffn_dim, dim)
+        self.ffn2 = lin(dim, ffn_dim)
+        self.norm_q = (1 + 0.1 * torch.randn(dim, generator=generator)).to(torch.bfloat16).to(device)
+        self.norm_k = (1 + 0.1 * torch.randn(dim, generator=generator)).to(torch.bfloat16).to(device)
+        self.modulation = (0.1 * torch.randn(1, 6, dim, generator=generator)).to(torch.bfloat16).to(device)
+
+
+class _Lin:
+    """Adapter giving gemm_gelu_quant_fp8 the FP8Linear fields it reads."""
+
+    def __init__(self, q, s, b):
+        self.weight, self.w_scale, self.bias = q, s, b
+
+
+def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor, cs: torch.Tensor,
+                      index, tok_map: torch.Tensor, heads: int = 12, eps: float = 1e-6):
+    """x [1, L, dim] bf16 (raster order) -> [1, L, dim].  ``index`` is the
+    device block index (sel, cnt, maxk) of the attention mask; ``tok_map``
+    is window_token_map(f, h, w); ``cs`` the (cos, sin) table [L, 64, 2]."""
+    B, L, D = x.shape
+    hd = D // heads
+    mod = (wts.modulation + t_mod).contiguous()
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = [
+        mod[:, i:i + 1].contiguous() for i in range(6)]
+
+    x8, xs = fused_ln_modulate_quant(x, scale_msa, shift_msa, eps)
+    qkv = fp8_gemm(x8, xs, *wts.qkv)                      # [L, 3D]
+    q = qkv[:, :D].view(B, L, D)
+    k = qkv[:, D:2 * D].view(B, L, D)
+    fused_rms_rope_qk(q, k, wts.norm_q, wts.norm_k, cs, eps=eps, head_dim=hd, inplace=True)
+
+    attn = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    block_sparse_attention_strided(
+        qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], None, 1.0 / math.sqrt(hd), heads=heads,
+        head_dim=hd, q_strides=(3 * D, hd), kv_strides=(3 * D, hd), out=attn,
+        o_strides=(D, hd), q_map=tok_map, kv_map=tok_map, index=index)
+
+    a8, as_ = quantize_fp8(attn, per_token=True)
+    x1 = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    fp8_gemm(a8, as_, *wts.o, out=x1, epilogue=_lib.EPI_GATE_ADD, res=x.view(L, D),
+             gate=gate_msa.view(D))
+
+    x8, xs = fused_ln_modulate_quant(x1.view(B, L, D), scale_mlp, shift_mlp, eps)
+    h8, hs = gemm_gelu_quant_fp8(x8, xs, _Lin(*wts.ffn0), per_token=True)
+    x2 = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    fp8_gemm(h8, hs, *wts.ffn2, out=x2, epilogue=_lib.EPI_GATE_ADD, res=x1, gate=gate_mlp.view(D))
+    return x2.view(B, L, D)
+
+
+class DiTStack:
+    """``blocks`` DiT blocks with random-init weights (~N(0, 0.02), per-channel
+    e4m3), the BASELINE C5 workload: one call = one streaming chunk."""
+
+    def __init__(self, blocks: int = 30, dim: int = 1536, heads: int = 12, ffn_dim: int = 8960,
+                 device="cuda", seed: int = 0):
+        g = torch.Generator().manual_seed(seed)
+        self.heads = heads
+        self.weights = [DiTBlockWeights(dim, ffn_dim, device, g) for _ in range(blocks)]
+
+    def __call__(self, x, t_mod, cs, index, tok_map):
+        for w in self.weights:
+            x = dit_block_forward(x, w, t_mod, cs, index, tok_map, self.heads)
+        return x
+
+
+__all__ = ["window_token_map", "DiTBlockWeights", "dit_block_forward", "DiTStack", "FP8Linear"]

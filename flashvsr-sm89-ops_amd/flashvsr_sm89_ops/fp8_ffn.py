@@ -1,0 +1,100 @@
+"""FFN with the GELU(tanh) -> FP8 mid-section fused into the FP8 GEMMs.
+
+The reference (flashvsr_sm89_ops/fp8_ffn.py:75-96) runs
+quantize -> mm0 -> [gelu+absmax] -> [gelu+quantize] -> mm2.  Here mm0's
+epilogue applies bias + bf16 rounding + tanh-GELU (rounded to bf16) and writes
+|GELU| maxima per (row, 128-column slab); one quantisation pass then turns the
+bf16 GELU rows into e4m3 codes with the reduced amax, and mm2 consumes them.
+The FP8 codes are those of ``quantize_fp8(gelu(h))`` for the bf16 h the GEMM
+produced: the epilogue and ``fused_gelu_quant_fp8`` share one GELU routine
+(exp by Cody-Waite reduction + Taylor polynomial, 1 - 2/(exp(2u)+1) as in the
+reference, fp8_ffn.py:24-30).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .fp8_linear import FP8Linear, fp8_gemm
+from .fp8_quant import FP8_MAX, _workspace, quantize_fp8  # noqa: F401
+
+
+def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
+    """y2: [M, K] bf16 -> (e4m3 codes of gelu_tanh(y2), scale), the bf16 GELU
+    never materialised (fp8_ffn.py:57-72)."""
+    _lib.require_gpu(y2)
+    _lib.require_dtype(y2, torch.bfloat16, "y2")
+    M, K = y2.shape
+    if y2.numel() and y2.stride(1) != 1:
+        y2 = y2.contiguous()
+    x8 = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=y2.device)
+    s = (torch.empty((M, 1), dtype=torch.float32, device=y2.device) if per_token
+         else torch.zeros(1, dtype=torch.float32, device=y2.device))
+    if y2.numel() == 0:
+        return x8, s
+    mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
+    ws = _workspace(y2, M, K, mode)
+    _lib.check(_lib.lib().fvsr_quant_fp8(y2.data_ptr(), M, K, y2.stride(0), mode, 1,
+                                         x8.data_ptr(), s.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream(y2)), "fused_gelu_quant_fp8")
+    return x8, s
+
+
+def gemm_gelu_quant_fp8(x8: torch.Tensor, s: torch.Tensor, lin: FP8Linear, per_token: bool):
+    """mm0 with the GELU epilogue, then the requantisation of its bf16 output:
+    returns (codes, scale) of quantize_fp8(gelu(bf16(x8 @ W.T * s * w_scale + b)))."""
+    M = x8.shape[0]
+    N = lin.weight.shape[0]
+    nparts = int(_lib.lib().fvsr_gemm_amax_parts(N))
+    amax = torch.empty((M, nparts), dtype=torch.float32, device=x8.device)
+    g = fp8_gemm(x8, s, lin.weight, lin.w_scale, lin.bias, epilogue=_lib.EPI_GELU,
+                 amax_part=amax)
+    h8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x8.device)
+    hs = (torch.empty((M, 1), dtype=torch.float32, device=x8.device) if per_token
+          else torch.zeros(1, dtype=torch.float32, device=x8.device))
+    mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
+    ws = _workspace(g, M, N, mode)
+    _lib.check(_lib.lib().fvsr_quant_fp8_from_amax(g.data_ptr(), M, N, amax.data_ptr(), nparts,
+                                                   mode, h8.data_ptr(), hs.data_ptr(),
+                                                   ws.data_ptr(), ws.numel(), _lib.stream(g)),
+               "gelu requantisation")
+    return h8, hs
+
+
+class FP8FFN(nn.Module):
+    """Drop-in for a DiT FFN `Sequential(Linear, GELU(tanh), Linear)` whose two
+    Linears are already FP8Linear (fp8_ffn.py:75-96)."""
+
+    def __init__(self, lin0, lin2):
+        super().__init__()
+        self.lin0 = lin0
+        self.lin2 = lin2
+
+    def forward(self, x):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        per_token = getattr(self.lin0, "per_token", False)
+        x8, s = quantize_fp8(x2, per_token=per_token)
+        h8, hs = gemm_gelu_quant_fp8(x8, s, self.lin0, per_token)
+        out = self.lin2._mm(h8, hs)
+        return out.reshape(*shape[:-1], out.shape[-1])
+
+
+def convert_ffn_fp8(model: nn.Module) -> int:
+    """Swap every `blocks.i.ffn` Sequential for FP8FFN; returns the count.
+    Requires convert_linears_fp8(model, parts=["ffn"]) first (fp8_ffn.py:99-115)."""
+    import re
+    pat = re.compile(r"^blocks\.\d+\.ffn$")
+    n = 0
+    for name, mod in list(model.named_modules()):
+        if not pat.match(name):
+            continue
+        l0, l2 = mod[0], mod[2]
+        assert type(l0).__name__ == "FP8Linear" and type(l2).__name__ == "FP8Linear", \
+            f"{name}: run convert_linears_fp8(parts=['ffn']) first"
+        parent_name, _, leaf = name.rpartition(".")
+        parent = model.get_submodule(parent_name)
+        setattr(parent, leaf, FP8FFN(l0, l2))
+        n += 1
+    return n

@@ -1,0 +1,116 @@
+"""FP8 (e4m3fn) Linear on CDNA4 FP8 matrix cores.
+
+`FP8Linear` mirrors the reference module (flashvsr_sm89_ops/fp8_linear.py:16-42):
+the weight is quantised once at conversion (``.weight`` float8_e4m3fn [N, K],
+``.w_scale`` fp32, ``.bias`` bf16 kept), activations are quantised on every
+forward, and ``_mm(x8, s)`` is the scaled GEMM with bias and bf16 output.
+The GEMM is the hand-written gfx950 kernel behind ``fvsr_fp8_gemm``.
+
+Scale granularity is per tensor by default, as in the reference.
+``per_channel=True`` quantises the weight per output channel and
+``per_token=True`` the activations per row (the BASELINE configurations).
+"""
+from __future__ import annotations
+
+import re
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .fp8_quant import FP8_MAX, quantize_fp8, quantize_weight_fp8  # noqa: F401
+
+
+def fp8_gemm(x8: torch.Tensor, s: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
+             bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
+             epilogue: int = _lib.EPI_BIAS, amax_part: torch.Tensor | None = None,
+             res: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(x8 @ w8.T * s * w_scale + bias): x8 [M,K] e4m3, w8 [N,K] e4m3,
+    s [1]/[M]/[M,1] fp32, w_scale 0-dim/[1]/[N] fp32, bias [N] bf16 or None."""
+    _lib.require_gpu(x8, s, w8, w_scale, bias, out, res, gate)
+    _lib.require_dtype(x8, torch.float8_e4m3fn, "x8")
+    _lib.require_dtype(w8, torch.float8_e4m3fn, "weight")
+    M, K = x8.shape
+    N, K2 = w8.shape
+    if K != K2:
+        raise ValueError(f"fp8_gemm: K mismatch {K} vs {K2}")
+    if x8.stride(1) != 1:
+        x8 = x8.contiguous()
+    if w8.stride(1) != 1:
+        w8 = w8.contiguous()
+    sa_mode = _lib.SCALE_ROW if s.numel() == M and M != 1 else _lib.SCALE_TENSOR
+    sb_mode = _lib.SCALE_ROW if w_scale.numel() == N and N != 1 else _lib.SCALE_TENSOR
+    if s.numel() not in (1, M) or w_scale.numel() not in (1, N):
+        raise ValueError("fp8_gemm: scale shapes must be per-tensor or per-row/column")
+    s = s.float().contiguous()
+    w_scale = w_scale.float().contiguous()
+    if bias is not None:
+        bias = bias.to(torch.bfloat16).contiguous()
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=x8.device)
+    rc = _lib.lib().fvsr_fp8_gemm(
+        x8.data_ptr(), x8.stride(0), s.data_ptr(), sa_mode,
+        w8.data_ptr(), w8.stride(0), w_scale.data_ptr(), sb_mode,
+        _lib.ptr(bias), out.data_ptr(), out.stride(0), M, N, K, epilogue,
+        _lib.ptr(amax_part), _lib.ptr(res), _lib.ptr(gate), _lib.stream(x8))
+    _lib.check(rc, "fp8_gemm")
+    return out
+
+
+class FP8Linear(nn.Module):
+    """Drop-in for the reference FP8Linear (fp8_linear.py:16-42)."""
+
+    def __init__(self, linear: nn.Linear, per_channel: bool = False, per_token: bool = False):
+        super().__init__()
+        w = linear.weight.detach()
+        q, s = quantize_weight_fp8(w.to(torch.bfloat16), per_channel=per_channel)
+        self.w_scale = s
+        self.weight = nn.Parameter(q, requires_grad=False)
+        if linear.bias is not None:
+            self.bias = nn.Parameter(linear.bias.detach().clone(), requires_grad=False)
+        else:
+            self.bias = None
+        self.per_channel = per_channel
+        self.per_token = per_token
+        self.in_features = w.shape[1]
+        self.out_features = w.shape[0]
+
+    def _mm(self, x8, s, out=None):
+        return fp8_gemm(x8, s, self.weight, self.w_scale, self.bias, out=out)
+
+    def forward(self, x):
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        x8, s = quantize_fp8(x2, per_token=self.per_token)
+        y = self._mm(x8, s)
+        return y.reshape(*shape[:-1], y.shape[-1])
+
+    def extra_repr(self):
+        g = "channel" if self.per_channel else "tensor"
+        a = "token" if self.per_token else "tensor"
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"weight_scale=per-{g}, act_scale=per-{a}, bias={self.bias is not None}")
+
+
+def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_channel: bool = False,
+                        per_token: bool = False) -> int:
+    """Convert DiT-block Linears whose module names match `parts`
+    ("ffn" / "self" / "cross"); returns the number converted
+    (fp8_linear.py:45-67).  Idempotent: FP8Linear is not an nn.Linear."""
+    allowed = []
+    if "self" in parts:
+        allowed.append(r"^blocks\.\d+\.self_attn\.[qkvo]$")
+    if "cross" in parts:
+        allowed.append(r"^blocks\.\d+\.cross_attn\.[qkvo]$")
+    if "ffn" in parts:
+        allowed.append(r"^blocks\.\d+\.ffn\.[02]$")
+    pats = [re.compile(p) for p in allowed]
+    n = 0
+    for name, mod in list(model.named_modules()):
+        if not isinstance(mod, nn.Linear) or not any(p.match(name) for p in pats):
+            continue
+        parent_name, _, leaf = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        setattr(parent, leaf, FP8Linear(mod, per_channel=per_channel, per_token=per_token))
+        n += 1
+    return n

@@ -1,0 +1,64 @@
+"""Dynamic FP8 (OCP e4m3fn) quantisation on gfx950.
+
+`quantize_fp8(x2)` keeps the reference contract (flashvsr_sm89_ops/fp8_quant.py:42-55):
+``s = max(amax,1e-12)/448; q = e4m3(clamp(x/s, +-448))`` with a true fp32
+divide, returning ``(q, amax/448)`` with the scale left on the device (no host
+sync).  ``per_token=True`` gives one scale per row (``[M, 1]``), the layout
+torch._scaled_mm takes for row-wise scales; per-token quantisation is a single
+HBM pass (one wavefront per row, the row stays in registers).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+FP8_MAX = 448.0
+
+
+def _workspace(x: torch.Tensor, rows: int, cols: int, mode: int) -> torch.Tensor:
+    n = int(_lib.lib().fvsr_quant_workspace_floats(rows, cols, mode))
+    return torch.empty(max(n, 1), dtype=torch.float32, device=x.device)
+
+
+def quantize_fp8(x2: torch.Tensor, per_token: bool = False):
+    """x2: [M, K] bf16 (rows may be strided, last dim contiguous) ->
+    (float8_e4m3fn [M, K], fp32 scale: [1] per tensor, [M, 1] per token)."""
+    _lib.require_gpu(x2)
+    _lib.require_dtype(x2, torch.bfloat16, "x2")
+    if x2.dim() != 2:
+        raise ValueError(f"quantize_fp8 expects a 2-D tensor, got shape {tuple(x2.shape)}")
+    M, K = x2.shape
+    if x2.numel() and x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x2.device)
+    if per_token:
+        s = torch.empty((M, 1), dtype=torch.float32, device=x2.device)
+    else:
+        s = torch.zeros(1, dtype=torch.float32, device=x2.device)
+    if x2.numel() == 0:
+        return q, s
+    mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
+    ws = _workspace(x2, M, K, mode)
+    _lib.check(_lib.lib().fvsr_quant_fp8(x2.data_ptr(), M, K, x2.stride(0), mode, 0,
+                                         q.data_ptr(), s.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream(x2)), "quantize_fp8")
+    return q, s
+
+
+def quantize_weight_fp8(w: torch.Tensor, per_channel: bool = False):
+    """Static weight quantisation of FP8Linear.__init__ (fp8_linear.py:17-22):
+    per tensor -> (q [N,K], 0-dim fp32 scale); per channel -> (q, [N] scales)."""
+    _lib.require_gpu(w)
+    _lib.require_dtype(w, torch.bfloat16, "weight")
+    w = w.contiguous()
+    N, K = w.shape
+    q = torch.empty((N, K), dtype=torch.float8_e4m3fn, device=w.device)
+    s = torch.empty(N if per_channel else 1, dtype=torch.float32, device=w.device)
+    if w.numel():
+        mode = _lib.SCALE_ROW if per_channel else _lib.SCALE_TENSOR
+        ws = _workspace(w, N, K, mode)
+        _lib.check(_lib.lib().fvsr_quant_weight_fp8(w.data_ptr(), N, K, mode, q.data_ptr(),
+                                                    s.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                    _lib.stream(w)), "quantize_weight_fp8")
+    return q, (s if per_channel else s.reshape(()))

@@ -1,0 +1,74 @@
+"""Fused AdaLN elementwise chains (bf16) on gfx950.
+
+`fused_ln_modulate(x, scale, shift)`: LayerNorm (no affine) then
+``x*(1+scale)+shift`` with eager's per-op bf16 roundings
+(flashvsr_sm89_ops/fused_adaln.py:22-42,60-71).  Note the argument order:
+(scale, shift), the reverse of upstream ``modulate(x, shift, scale)``.
+`fused_gate_add(x, gate, residual)`: ``bf16(x + bf16(gate*residual))``,
+bitwise equal to eager (fused_adaln.py:45-57,74-85).
+`fused_ln_modulate_quant` additionally returns the per-row e4m3 codes of the
+modulated rows from the same pass (the activation quantisation of the FP8
+linear that consumes them).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _check_params(x, *ps):
+    B, L, D = x.shape
+    _lib.require_dtype(x, torch.bfloat16, "x")
+    for p in ps:
+        _lib.require_dtype(p, torch.bfloat16, "modulation parameter")
+        if p.numel() != B * D:
+            raise ValueError(f"modulation parameter shape {tuple(p.shape)} does not match "
+                             f"[B, 1, D] = [{B}, 1, {D}]")
+
+
+def fused_ln_modulate(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                      eps: float = 1e-6):
+    """LayerNorm(affine=False) + modulate. x [B, L, D] contiguous bf16;
+    scale/shift [B, 1, D]."""
+    B, L, D = x.shape
+    assert x.is_contiguous() and scale.is_contiguous() and shift.is_contiguous()
+    _lib.require_gpu(x, scale, shift)
+    _check_params(x, scale, shift)
+    out = torch.empty_like(x)
+    _lib.check(_lib.lib().fvsr_ln_modulate(x.data_ptr(), scale.data_ptr(), shift.data_ptr(),
+                                           out.data_ptr(), B, L, D, float(eps), None, None,
+                                           _lib.stream(x)), "fused_ln_modulate")
+    return out
+
+
+def fused_ln_modulate_quant(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
+                            eps: float = 1e-6, write_bf16: bool = False):
+    """fused_ln_modulate + per-row e4m3 quantisation of its output in one pass.
+    Returns (codes [B*L, D] e4m3, row scales [B*L, 1] fp32[, bf16 out])."""
+    B, L, D = x.shape
+    assert x.is_contiguous() and scale.is_contiguous() and shift.is_contiguous()
+    _lib.require_gpu(x, scale, shift)
+    _check_params(x, scale, shift)
+    q = torch.empty((B * L, D), dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty((B * L, 1), dtype=torch.float32, device=x.device)
+    out = torch.empty_like(x) if write_bf16 else None
+    _lib.check(_lib.lib().fvsr_ln_modulate(x.data_ptr(), scale.data_ptr(), shift.data_ptr(),
+                                           _lib.ptr(out), B, L, D, float(eps), q.data_ptr(),
+                                           s.data_ptr(), _lib.stream(x)),
+               "fused_ln_modulate_quant")
+    return (q, s, out) if write_bf16 else (q, s)
+
+
+def fused_gate_add(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor):
+    """x + gate * residual. x/residual [B, L, D] contiguous bf16; gate [B, 1, D]."""
+    B, L, D = x.shape
+    assert x.is_contiguous() and residual.is_contiguous() and gate.is_contiguous()
+    _lib.require_gpu(x, gate, residual)
+    _lib.require_dtype(residual, torch.bfloat16, "residual")
+    _check_params(x, gate)
+    out = torch.empty_like(x)
+    _lib.check(_lib.lib().fvsr_gate_add(x.data_ptr(), gate.data_ptr(), residual.data_ptr(),
+                                        out.data_ptr(), B, L, D, _lib.stream(x)),
+               "fused_gate_add")
+    return out

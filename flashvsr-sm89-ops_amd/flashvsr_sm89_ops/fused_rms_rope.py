@@ -1,0 +1,106 @@
+"""Fused RMSNorm + RoPE (bf16) on gfx950.
+
+Same contract as the reference (flashvsr_sm89_ops/fused_rms_rope.py:21-83):
+RMS over the full hidden dim D in fp32, ``y = bf16(x*rsqrt(ms+eps)) * w``,
+then the interleaved pairs (2i, 2i+1) of every head are rotated with
+cos/sin[s, i] in fp32 and stored as bf16; ``rope=False`` is plain RMSNorm.
+
+The kernel reads (cos, sin) in the interleaved layout of
+``view_as_real(freqs_cis)`` (fp32 [S, head_dim/2, 2]), so a complex64
+freqs_cis is used without any copy; other dtypes are converted once and
+cached per freqs tensor.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_CS_CACHE: dict = {}
+_CS_CACHE_MAX = 8
+
+
+def _freqs_table(freqs: torch.Tensor) -> torch.Tensor:
+    """complex [..., S, head_dim/2] -> fp32 [S, head_dim/2, 2] contiguous (cos, sin)."""
+    f = freqs.reshape(-1, freqs.shape[-1])
+    if f.dtype == torch.complex64 and f.is_contiguous():
+        return torch.view_as_real(f)
+    key = (freqs.data_ptr(), tuple(freqs.shape), freqs.dtype, freqs.device,
+           getattr(freqs, "_version", 0))
+    t = _CS_CACHE.get(key)
+    if t is None:
+        t = torch.view_as_real(f.to(torch.complex64)).contiguous()
+        if len(_CS_CACHE) >= _CS_CACHE_MAX:
+            _CS_CACHE.pop(next(iter(_CS_CACHE)))
+        _CS_CACHE[key] = t
+    return t
+
+
+def _freqs_cos_sin(freqs: torch.Tensor):
+    """[..., S, 64] complex -> (cos [S, 64] fp32, sin [S, 64] fp32), as the
+    reference helper (fused_rms_rope.py:58-63)."""
+    t = _freqs_table(freqs)
+    return t[..., 0].contiguous(), t[..., 1].contiguous()
+
+
+def _table_for(freqs, L: int, head_dim: int, device) -> torch.Tensor:
+    if freqs is None:
+        raise ValueError("fused_rms_rope: rope=True needs freqs_cis")
+    if torch.is_tensor(freqs) and not torch.is_complex(freqs):
+        # Already a (cos, sin) interleaved fp32 table.
+        t = freqs.reshape(-1, head_dim // 2, 2).float().contiguous()
+    else:
+        t = _freqs_table(freqs)
+    if t.shape[0] < L or t.shape[1] != head_dim // 2:
+        raise ValueError(f"freqs table {tuple(t.shape)} does not cover L={L}, head_dim={head_dim}")
+    if t.device != device:
+        t = t.to(device)
+    return t
+
+
+def fused_rms_rope(x: torch.Tensor, weight: torch.Tensor, freqs_cis, eps: float = 1e-6,
+                   rope: bool = True, head_dim: int = 128):
+    """x [B, L, D] bf16 -> RMSNorm(weight) -> [x RoPE] (fused_rms_rope.py:66-83)."""
+    _lib.require_gpu(x, weight)
+    _lib.require_dtype(x, torch.bfloat16, "x")
+    B, L, D = x.shape
+    x2 = x.contiguous()
+    w = weight.to(torch.bfloat16).contiguous()
+    out = torch.empty_like(x2)
+    cs = _table_for(freqs_cis, L, head_dim, x.device) if rope else None
+    _lib.check(_lib.lib().fvsr_rms_rope(x2.data_ptr(), w.data_ptr(), _lib.ptr(cs),
+                                        out.data_ptr(), B, L, D, head_dim if rope else D,
+                                        float(eps), int(bool(rope)), _lib.stream(x)),
+               "fused_rms_rope")
+    return out
+
+
+def fused_rms_rope_qk(q: torch.Tensor, k: torch.Tensor, weight_q: torch.Tensor,
+                      weight_k: torch.Tensor, freqs_cis, eps: float = 1e-6, head_dim: int = 128,
+                      inplace: bool = False):
+    """Both self-attention RMSNorm+RoPE calls (integrate.py:59-62) in one launch.
+    q, k: [B, L, D] bf16 whose rows may be strided (e.g. column slices of a
+    fused QKV output, last dim contiguous).  ``inplace`` writes the results
+    over q and k."""
+    _lib.require_gpu(q, k, weight_q, weight_k)
+    B, L, D = q.shape
+    if k.shape != q.shape:
+        raise ValueError("fused_rms_rope_qk: q and k shapes differ")
+    if q.stride(-1) != 1 or k.stride(-1) != 1 or q.stride(1) != k.stride(1) or \
+            (B > 1 and (q.stride(0) != L * q.stride(1) or k.stride(0) != L * k.stride(1))):
+        q, k = q.contiguous(), k.contiguous()
+        inplace = False
+    wq = weight_q.to(torch.bfloat16).contiguous()
+    wk = weight_k.to(torch.bfloat16).contiguous()
+    cs = _table_for(freqs_cis, L, head_dim, q.device)
+    if inplace:
+        oq, ok = q, k
+    else:
+        oq = torch.empty((B, L, D), dtype=q.dtype, device=q.device)
+        ok = torch.empty((B, L, D), dtype=k.dtype, device=k.device)
+    _lib.check(_lib.lib().fvsr_rms_rope_qk(q.data_ptr(), k.data_ptr(), wq.data_ptr(),
+                                           wk.data_ptr(), cs.data_ptr(), oq.data_ptr(),
+                                           ok.data_ptr(), B, L, D, head_dim, float(eps),
+                                           q.stride(1), oq.stride(1), _lib.stream(q)),
+               "fused_rms_rope_qk")
+    return oq, ok

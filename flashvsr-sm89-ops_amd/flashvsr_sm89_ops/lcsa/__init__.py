@@ -1,0 +1,3 @@
+"""Block-sparse attention (LCSA) for the FlashVSR DiT: HIP kernels on gfx950."""
+from .hip_lcsa import (block_sparse_attention, block_sparse_attention_bhsd,  # noqa: F401
+                       block_sparse_attention_strided, build_csr)

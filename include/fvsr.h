@@ -1,0 +1,178 @@
+/*
+ * fvsr.h — C ABI of the MI355X (gfx950) FlashVSR DiT-block operator pack.
+ *
+ * One shared library, libfvsr.so, built from the HIP sources in
+ * flashvsr-sm89-ops_amd/csrc.
+ * The Python package flashvsr_sm89_ops binds these entry points with ctypes;
+ * any other host language can bind them the same way.
+ *
+ * Conventions shared by every entry point:
+ *  - Tensors are raw device pointers.  bf16 tensors hold uint16 bit patterns,
+ *    e4m3fn tensors hold uint8 codes (OCP e4m3fn, max 448, 0x7F = NaN),
+ *    scales are fp32.  Row-major, leading dimension = row length unless an
+ *    explicit stride is given.
+ *  - The library never allocates and never synchronises the host.  Outputs
+ *    and scratch ("workspace") are caller-owned; every kernel is enqueued on
+ *    the hipStream_t passed as `stream` (NULL = the default stream).
+ *  - Return value: FVSR_OK (0) or a negative fvsr_status.  Argument checks
+ *    run on the host before anything is enqueued.
+ *  - Reentrant: no mutable global state.
+ *
+ * Each declaration names the reference interface (aireet/flashvsr-sm89-ops,
+ * file:line) whose work it carries.
+ */
+#ifndef FVSR_H
+#define FVSR_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  FVSR_OK = 0,
+  FVSR_EINVAL = -1,       /* bad shape, stride, pointer or mode */
+  FVSR_EHIP = -2,         /* a HIP launch failed (hipGetLastError) */
+  FVSR_EUNSUPPORTED = -3, /* valid arguments outside what the kernels cover */
+  FVSR_EWORKSPACE = -4    /* workspace too small */
+} fvsr_status;
+
+/* Granularity of an activation or weight scale. */
+enum { FVSR_SCALE_TENSOR = 0, FVSR_SCALE_ROW = 1 };
+
+/* GEMM epilogues. */
+enum {
+  FVSR_EPI_BIAS = 0,     /* C = bf16(acc*sa*sb + bias)                                  */
+  FVSR_EPI_GELU = 1,     /* C = bf16(gelu_tanh(bf16(acc*sa*sb + bias))), plus |C| maxima
+                            per (row, 128-column slab) into `amax_part`                  */
+  FVSR_EPI_GATE_ADD = 2  /* C = bf16(res + bf16(gate[n] * bf16(acc*sa*sb + bias)))      */
+};
+
+/* Library version string ("fvsr <semver> gfx950"). */
+const char* fvsr_version(void);
+
+/* Number of 32-bit floats of workspace quant entry points need. */
+int64_t fvsr_quant_workspace_floats(int64_t rows, int64_t cols, int mode);
+
+/*
+ * Dynamic e4m3 quantisation of a bf16 [rows, cols] matrix (row stride ld
+ * elements), optionally of tanh-GELU(x) (gelu = 1).
+ *   mode FVSR_SCALE_TENSOR: one scale, reference quantize_fp8
+ *     (flashvsr_sm89_ops/fp8_quant.py:42-55) and fused_gelu_quant_fp8
+ *     (fp8_ffn.py:57-72); scale_out[0] = amax/448.
+ *   mode FVSR_SCALE_ROW: one scale per row, scale_out[rows].
+ * codes: uint8 [rows, cols] contiguous.  workspace: fvsr_quant_workspace_floats.
+ */
+int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mode, int gelu,
+                   void* codes, float* scale_out, float* workspace, int64_t workspace_floats,
+                   void* stream);
+
+/*
+ * Quantisation whose amax is already known as partial maxima: row r's amax is
+ * max(amax_part[r*nparts + 0 .. nparts-1]) (FVSR_SCALE_ROW) or the max over
+ * all rows*nparts entries (FVSR_SCALE_TENSOR).  Used after an FVSR_EPI_GELU
+ * GEMM: together they carry fused_gelu_quant_fp8 (fp8_ffn.py:57-72).
+ */
+int fvsr_quant_fp8_from_amax(const void* x, int64_t rows, int64_t cols, const float* amax_part,
+                             int64_t nparts, int mode, void* codes, float* scale_out,
+                             float* workspace, int64_t workspace_floats, void* stream);
+
+/*
+ * Static weight quantisation, reference FP8Linear.__init__
+ * (flashvsr_sm89_ops/fp8_linear.py:17-22).  mode FVSR_SCALE_TENSOR keeps the
+ * eager bf16 roundings: s = fp32(bf16(amax/448) clamped at bf16(1e-12)),
+ * q = e4m3(bf16(w/s)); FVSR_SCALE_ROW is the per-output-channel form,
+ * q = e4m3(w/s_n) in fp32.  w: bf16 [n, k]; codes uint8 [n, k]; scale_out
+ * [1] or [n]; workspace: fvsr_quant_workspace_floats(n, k, mode).
+ */
+int fvsr_quant_weight_fp8(const void* w, int64_t n, int64_t k, int mode, void* codes,
+                          float* scale_out, float* workspace, int64_t workspace_floats,
+                          void* stream);
+
+/*
+ * FP8 GEMM, C[M,N] = epilogue(sum_k A[m,k]*B[n,k]) with A e4m3 [M,K] (row
+ * stride lda bytes) and B e4m3 [N,K] (row stride ldb bytes) — the
+ * torch._scaled_mm(x8, W8.t(), scale_a, scale_b, bias, bf16) call of
+ * FP8Linear._mm (fp8_linear.py:28-30).  sa: [1] or [M] (sa_mode), sb: [1] or
+ * [N] (sb_mode).  bias: bf16 [N] or NULL.  C: bf16 [M,N] row stride ldc.
+ * K must be a multiple of 16 and lda/ldb multiples of 16.
+ * epilogue FVSR_EPI_GELU also needs amax_part (float [M, ceil(N/128)]);
+ * FVSR_EPI_GATE_ADD needs res (bf16 [M,N], row stride ldc) and gate (bf16 [N]).
+ */
+int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa_mode,
+                  const void* b, int64_t ldb, const float* sb, int sb_mode,
+                  const void* bias, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                  int epilogue, float* amax_part, const void* res, const void* gate,
+                  void* stream);
+
+/* Number of 128-column slabs FVSR_EPI_GELU writes per row: ceil(N/128). */
+int64_t fvsr_gemm_amax_parts(int64_t N);
+
+/*
+ * LayerNorm (no affine) + modulate, reference fused_ln_modulate
+ * (flashvsr_sm89_ops/fused_adaln.py:22-42,60-71): x bf16 [B,L,D];
+ * scale/shift bf16 [B,1,D].  out (bf16 [B,L,D]) may be NULL when codes is
+ * given: then only the per-row e4m3 quantisation of the modulated rows is
+ * written (codes uint8 [B*L, D], row_scale float [B*L]) — the activation
+ * quantisation of the FP8 linear that consumes it, fused into the same pass.
+ */
+int fvsr_ln_modulate(const void* x, const void* scale, const void* shift, void* out,
+                     int64_t B, int64_t L, int64_t D, float eps, void* codes, float* row_scale,
+                     void* stream);
+
+/* out = bf16(x + bf16(gate*res)), reference fused_gate_add
+ * (fused_adaln.py:45-57,74-85): x, res, out bf16 [B,L,D]; gate bf16 [B,1,D]. */
+int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out, int64_t B,
+                  int64_t L, int64_t D, void* stream);
+
+/*
+ * RMSNorm over D + interleaved RoPE per head, reference fused_rms_rope
+ * (flashvsr_sm89_ops/fused_rms_rope.py:21-83).  x, out: bf16 [B,L,D];
+ * weight bf16 [D]; cs: fp32 [L, head_dim/2, 2] (cos, sin) pairs — the
+ * view_as_real of the complex freqs_cis — or NULL with rope = 0.
+ * Position of row r is r % L.
+ */
+int fvsr_rms_rope(const void* x, const void* weight, const float* cs, void* out, int64_t B,
+                  int64_t L, int64_t D, int64_t head_dim, float eps, int rope, void* stream);
+
+/* Both self-attention projections in one launch (q and k share the cos/sin
+ * reads): the two fused_rms_rope calls of integrate.py:59-62.  Rows of q/k
+ * are ld_in elements apart and rows of out_q/out_k ld_out apart (column
+ * slices of a fused QKV projection; in place is allowed).  Requires
+ * D % 8 == 0, D <= 1536, head_dim % 8 == 0 and 16-byte aligned rows. */
+int fvsr_rms_rope_qk(const void* q, const void* k, const void* wq, const void* wk,
+                     const float* cs, void* out_q, void* out_k, int64_t B, int64_t L, int64_t D,
+                     int64_t head_dim, float eps, int64_t ld_in, int64_t ld_out, void* stream);
+
+/*
+ * Block index from a bool block mask, reference build_csr
+ * (flashvsr_sm89_ops/lcsa/triton_lcsa.py:64-71) without its host sync:
+ * keep uint8 [H, NQ, NK] -> sel int32 [H, NQ, NK] (kept block ids ascending,
+ * the rest of each row unspecified) and cnt int32 [H, NQ].
+ */
+int fvsr_block_index(const uint8_t* keep, int64_t H, int64_t NQ, int64_t NK, int32_t* sel,
+                     int32_t* cnt, void* stream);
+
+/*
+ * Block-sparse attention over 128-token blocks, reference _bsa_fwd_kernel /
+ * block_sparse_attention (lcsa/triton_lcsa.py:19-61,74-94): for each head h
+ * and query block i, softmax(Q_i K_J^T * sm_scale) V_J over the kept key
+ * blocks J = sel[h,i,0..cnt[h,i]-1]; rows with cnt 0 are written as zeros.
+ * q/k/v/o bf16, element (token t, head h, dim d) at ptr[t*tok_stride +
+ * h*head_stride + d]; head_dim must be 128; sel row stride is maxk.
+ * tok_map: NULL, or int32 [NQ*128] (queries/outputs) and [NK*128] (keys) maps
+ * from block-order position to stored token index (kmap), letting raster-order
+ * tensors be read in window order without a copy.
+ */
+int fvsr_bsa_fwd(const void* q, const void* k, const void* v, void* o, int64_t q_tok_stride,
+                 int64_t q_head_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+                 int64_t o_tok_stride, int64_t o_head_stride, const int32_t* sel,
+                 const int32_t* cnt, int64_t maxk, int64_t H, int64_t NQ, int64_t NK,
+                 int64_t head_dim, float sm_scale, const int32_t* q_map, const int32_t* kv_map,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FVSR_H */

@@ -1,0 +1,183 @@
+/*
+ * CPU oracle for the FlashVSR DiT-block operator pack: the byte-exact parts.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP kernels
+ * are compared against; it is loaded by tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg, never by the product path.
+ *
+ * Build: oracle/build_oracle.sh (gcc -O2 -ffp-contract=off, SSE float math,
+ * so every float operation below is one IEEE-754 binary32 operation).
+ *
+ * What each function restates (reference = aireet/flashvsr-sm89-ops):
+ *   orc_e4m3_encode   fp32 -> OCP e4m3fn, round-to-nearest-even, |x|>=480 or
+ *                     (464,480) -> NaN code 0x7F|sign.  Same semantics as the
+ *                     `.to(tl.float8e4nv)` store in flashvsr_sm89_ops/fp8_quant.py:35
+ *                     and torch's float8_e4m3fn cast.
+ *   orc_quant_rows    contract Q-A: amax -> s = max(amax,1e-12)/448 ->
+ *                     e4m3(clamp(x/s, +-448)), returned scale amax/448
+ *                     (fp8_quant.py:16-35,42-55), per tensor or per row.
+ *   orc_gelu_bf16     tanh-GELU through 1-2/(exp(2u)+1), rounded to bf16
+ *                     (fp8_ffn.py:24-30), with orc_expf as the exp.
+ *   orc_expf          fp32 exp by Cody-Waite reduction + degree-7 Taylor
+ *                     polynomial (W. J. Cody, W. Waite, "Software Manual for
+ *                     the Elementary Functions", 1980), mul/add only.  The HIP
+ *                     kernels run the same operation sequence, so the GELU
+ *                     values (and therefore the FP8 codes) are bit-identical.
+ *   orc_quant_weight  contract Q-W: per-tensor (fp8_linear.py:17-22, with the
+ *                     bf16 intermediate roundings of eager type promotion) and
+ *                     per-output-channel (fp32 division, single rounding).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* bf16 round-to-nearest-even of an fp32 value, returned as fp32. NaN stays NaN. */
+static inline float bf16r(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return u2f((u | 0x00400000u) & 0xffff0000u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return u2f(u & 0xffff0000u);
+}
+static inline float bf2f(uint16_t h) { return u2f((uint32_t)h << 16); }
+static inline uint16_t f2bf(float f) { return (uint16_t)(f2u(bf16r(f)) >> 16); }
+
+uint8_t orc_e4m3_one(float f) {
+    uint32_t u = f2u(f);
+    uint8_t sign = (uint8_t)((u >> 24) & 0x80u);
+    uint32_t a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return sign | 0x7f;          /* NaN */
+    if (a >= 0x43f00000u) return sign | 0x7f;         /* >= 480: no inf in e4m3fn */
+    if (a < 0x3c800000u) {                            /* < 2^-6: subnormal grid 2^-9 */
+        float scaled = u2f(a) * 512.0f;               /* exact: power-of-two scale */
+        int m = (int)nearbyintf(scaled);              /* ties-to-even (default mode) */
+        return sign | (uint8_t)m;                     /* m == 8 is the min normal */
+    }
+    a += 0x7ffffu + ((a >> 20) & 1u);                 /* RNE to 3 mantissa bits */
+    return sign | (uint8_t)((a >> 20) - (120u << 3)); /* rebias 127 -> 7 */
+}
+
+float orc_e4m3_value(uint8_t c) {
+    int s = c & 0x80, e = (c >> 3) & 15, m = c & 7;
+    float v;
+    if (e == 15 && m == 7) return NAN;
+    v = e == 0 ? ldexpf((float)m, -9) : ldexpf(1.0f + (float)m / 8.0f, e - 7);
+    return s ? -v : v;
+}
+
+void orc_e4m3_encode(const float* x, uint8_t* q, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) q[i] = orc_e4m3_one(x[i]);
+}
+
+void orc_e4m3_decode(const uint8_t* q, float* x, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) x[i] = orc_e4m3_value(q[i]);
+}
+
+void orc_bf16_round(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = bf16r(x[i]);
+}
+
+/* exp(x) in binary32: n = rint(x*log2e); r = (x - n*ln2_hi) - n*ln2_lo;
+ * p = Taylor_7(r) in Horner form; result = p * 2^n (two exact power-of-two
+ * multiplies so 2^n never overflows the exponent field on its own). */
+float orc_expf(float x) {
+    const float LOG2E = 1.44269502162933349609375f;
+    const float LN2_HI = 0.693145751953125f;          /* 11 significant bits: n*LN2_HI exact */
+    const float LN2_LO = 1.428606765330187045e-06f;
+    if (x != x) return x;
+    if (x > 88.7228394f) return INFINITY;
+    if (x < -103.972084f) return 0.0f;
+    float t = x * LOG2E;
+    float n = nearbyintf(t);
+    float r = x - n * LN2_HI;
+    r = r - n * LN2_LO;
+    float p = 1.984126984126984e-04f;                 /* 1/7! */
+    p = p * r + 1.388888888888889e-03f;               /* 1/6! */
+    p = p * r + 8.333333333333333e-03f;               /* 1/5! */
+    p = p * r + 4.166666666666666e-02f;               /* 1/4! */
+    p = p * r + 1.666666666666667e-01f;               /* 1/3! */
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    int ni = (int)n;
+    int h = ni / 2;
+    float s1 = u2f((uint32_t)(h + 127) << 23);
+    float s2 = u2f((uint32_t)(ni - h + 127) << 23);
+    return (p * s1) * s2;
+}
+
+/* tanh-GELU of one bf16-valued input, result rounded to bf16 (as fp32).
+ * Operation order follows fp8_ffn.py:26-30 left to right. */
+float orc_gelu_one(float x) {
+    const float C0 = 0.7978845608028654f;
+    float u = C0 * (x + ((0.044715f * x) * x) * x);
+    float t = 1.0f - 2.0f / (orc_expf(2.0f * u) + 1.0f);
+    float g = (0.5f * x) * (1.0f + t);
+    return bf16r(g);
+}
+
+void orc_gelu_bf16(const uint16_t* h, uint16_t* g, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) g[i] = f2bf(orc_gelu_one(bf2f(h[i])));
+}
+
+/* Q-A over a [rows, cols] bf16 matrix (leading dimension ld elements).
+ * per_row = 0: one scale for the whole matrix (scale[0]); per_row = 1: one per row.
+ * gelu = 1 quantises gelu(x) instead of x (fp8_ffn.py:43-54). */
+void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
+                    int per_row, int gelu, uint8_t* q, float* scale_out) {
+    const float FP8_MAX = 448.0f;
+    int64_t groups = per_row ? rows : 1;
+    int64_t rpg = per_row ? 1 : rows;
+    for (int64_t g = 0; g < groups; ++g) {
+        float amax = 0.0f;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < cols; ++c) {
+                float v = bf2f(x[r * ld + c]);
+                if (gelu) v = orc_gelu_one(v);
+                v = fabsf(v);
+                if (v > amax) amax = v;
+            }
+        float s = (amax > 1e-12f ? amax : 1e-12f) / FP8_MAX;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < cols; ++c) {
+                float v = bf2f(x[r * ld + c]);
+                if (gelu) v = orc_gelu_one(v);
+                v = v / s;
+                v = v < -FP8_MAX ? -FP8_MAX : v;
+                v = v > FP8_MAX ? FP8_MAX : v;
+                q[r * cols + c] = orc_e4m3_one(v);
+            }
+        scale_out[g] = amax / FP8_MAX;
+    }
+}
+
+/* Q-W.  per_channel = 0 (fp8_linear.py:20-22):
+ *   w_scale = fp32(bf16(bf16(amax) / 448).clamp_min(bf16(1e-12)))
+ *   q = e4m3(bf16(fp32(w) / w_scale))
+ * per_channel = 1 (row-wise generalisation, bf16[N,K] / fp32[N,1] promotes to fp32):
+ *   s_n = fp32(bf16(amax_n / 448).clamp_min(bf16(1e-12)));  q = e4m3(fp32(w) / s_n) */
+void orc_quant_weight(const uint16_t* w, int64_t n, int64_t k, int per_channel,
+                      uint8_t* q, float* scale_out) {
+    const float lo = bf16r(1e-12f);
+    int64_t groups = per_channel ? n : 1;
+    int64_t rpg = per_channel ? 1 : n;
+    for (int64_t g = 0; g < groups; ++g) {
+        float amax = 0.0f;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < k; ++c) {
+                float v = fabsf(bf2f(w[r * k + c]));
+                if (v > amax) amax = v;
+            }
+        float s = bf16r(amax / 448.0f);
+        if (s < lo) s = lo;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < k; ++c) {
+                float v = bf2f(w[r * k + c]) / s;
+                if (!per_channel) v = bf16r(v);
+                q[r * k + c] = orc_e4m3_one(v);
+            }
+        scale_out[g] = s;
+    }
+}

@@ -1,0 +1,436 @@
+"""GPU parity: every HIP kernel (through libfvsr.so's C ABI, via the package
+wrappers) against the CPU oracle on the same seeded inputs.
+
+Bars: FP8 codes and scales bit-exact; gate_add bitwise; GELU values bitwise
+(shared exp); bf16 outputs within rtol 2e-2 / atol 2e-2 (plus a tighter
+mismatch-fraction check); attention max-abs-err <= 1e-2.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLD = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def ops():
+    import flashvsr_sm89_ops as f
+    return f
+
+
+def dev_bf16(bits):
+    t = torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16)
+    return t.to(DEV)
+
+
+def host_bits(t):
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def host_f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def host_codes(t):
+    return t.detach().contiguous().view(torch.uint8).cpu().numpy()
+
+
+def rnd_bits(shape, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    return O.bf16_bits(rng.standard_normal(shape).astype(np.float32) * np.float32(scale))
+
+
+def codes_dev(c):
+    return torch.from_numpy(np.ascontiguousarray(c)).view(torch.float8_e4m3fn).to(DEV)
+
+
+# ----------------------------------------------------------------------------- quantisation
+
+QSHAPES = [(4224, 1536), (33, 8960), (7, 1000), (5, 1003), (3, 24), (1, 8), (0, 1536)]
+
+
+@pytest.mark.parametrize("shape", QSHAPES)
+@pytest.mark.parametrize("per_token", [True, False])
+def test_quantize_fp8_bitexact(ops, shape, per_token):
+    x = rnd_bits(shape, seed=shape[0] * 7 + shape[1], scale=4.0)
+    if shape[0] > 2:
+        x[1] = 0  # all-zero row
+        x[2, 0] = O.bf16_bits(np.float32([1e4]))[0]  # outlier
+    q, s = ops.quantize_fp8(dev_bf16(x), per_token=per_token)
+    torch.cuda.synchronize()
+    if shape[0] == 0:
+        assert q.shape == shape
+        return
+    rq, rs = O.quantize_fp8(x, per_row=per_token)
+    assert np.array_equal(host_codes(q), rq)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_quantize_golden(ops):
+    x = dev_bf16(GOLD["quant_x"].reshape(48, 1536))
+    q, s = ops.quantize_fp8(x)
+    assert np.array_equal(host_codes(q).reshape(-1), GOLD["quant_tensor_q"].reshape(-1))
+    assert np.array_equal(host_f(s), GOLD["quant_tensor_s"])
+    q, s = ops.quantize_fp8(x, per_token=True)
+    assert np.array_equal(host_codes(q).reshape(-1), GOLD["quant_row_q"].reshape(-1))
+    assert np.array_equal(host_f(s).reshape(-1), GOLD["quant_row_s"])
+
+
+def test_quantize_strided_rows(ops):
+    x = rnd_bits((64, 2048), seed=11)
+    xd = dev_bf16(x)[:, 256:256 + 1536]  # row stride 2048, last dim contiguous
+    q, s = ops.quantize_fp8(xd, per_token=True)
+    rq, rs = O.quantize_fp8(np.ascontiguousarray(x[:, 256:256 + 1536]), per_row=True)
+    assert np.array_equal(host_codes(q), rq) and np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_e4m3_conversion_all_bf16_patterns(ops):
+    """Every finite bf16 value quantised with scale 1 (amax pinned at 448 by an
+    extra element) against the oracle encoder: RNE, subnormals, saturation."""
+    b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = O.from_bf16_bits(b)
+    keep = np.isfinite(f) & (np.abs(f) <= 448)
+    vals = O.bf16_bits(np.concatenate([f[keep], np.float32([448.0])]))
+    pad = (-len(vals)) % 8
+    vals = np.concatenate([vals, np.zeros(pad, np.uint16)])
+    q, s = ops.quantize_fp8(dev_bf16(vals.reshape(1, -1)), per_token=True)
+    assert host_f(s).reshape(-1)[0] == 1.0
+    assert np.array_equal(host_codes(q).reshape(-1), O.e4m3_encode(O.from_bf16_bits(vals)))
+
+
+@pytest.mark.parametrize("shape", [(64, 8960), (5, 1003), (16, 1024)])
+@pytest.mark.parametrize("per_token", [True, False])
+def test_gelu_quant_bitexact(ops, shape, per_token):
+    h = rnd_bits(shape, seed=99 + shape[1], scale=3.0)
+    q, s = ops.fused_gelu_quant_fp8(dev_bf16(h), per_token=per_token)
+    rq, rs = O.quantize_fp8(h, per_row=per_token, gelu=True)
+    assert np.array_equal(host_codes(q), rq)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+
+
+@pytest.mark.parametrize("shape", [(1536, 1536), (96, 256), (8960, 1536), (7, 100)])
+@pytest.mark.parametrize("per_channel", [True, False])
+def test_weight_quant_bitexact(ops, shape, per_channel):
+    w = rnd_bits(shape, seed=shape[0], scale=0.02)
+    q, s = ops.quantize_weight_fp8(dev_bf16(w), per_channel=per_channel)
+    rq, rs = O.quantize_weight(w, per_channel=per_channel)
+    assert np.array_equal(host_codes(q), rq)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_weight_quant_golden(ops):
+    w = dev_bf16(GOLD["wq_w"].reshape(96, 256))
+    q, s = ops.quantize_weight_fp8(w)
+    assert np.array_equal(host_codes(q).reshape(-1), GOLD["wq_tensor_q"].reshape(-1))
+    assert host_f(s).reshape(-1)[0] == GOLD["wq_tensor_s"][0]
+    q, s = ops.quantize_weight_fp8(w, per_channel=True)
+    assert np.array_equal(host_codes(q).reshape(-1), GOLD["wq_channel_q"].reshape(-1))
+
+
+# ----------------------------------------------------------------------------- GEMM
+
+def _gemm_inputs(M, N, K, seed):
+    rng = np.random.default_rng(seed)
+    a = O.e4m3_encode(rng.standard_normal((M, K)).astype(np.float32) * 40)
+    b = O.e4m3_encode(rng.standard_normal((N, K)).astype(np.float32) * 40)
+    sa = (rng.random(M) * 0.01 + 1e-3).astype(np.float32)
+    sb = (rng.random(N) * 0.01 + 1e-3).astype(np.float32)
+    bias = O.bf16_bits(rng.standard_normal(N).astype(np.float32))
+    return a, b, sa, sb, bias
+
+
+def _ulp_dist(out, ref):
+    """Distance in bf16 units in the last place (sign-magnitude bit order)."""
+    def key(x):
+        b = O.bf16_bits(x).astype(np.int32)
+        return np.where(b & 0x8000, -(b & 0x7FFF), b)
+    return np.abs(key(out) - key(ref))
+
+
+def _close_bf16(out, ref, frac=0.05, max_ulp=1):
+    """North-star tolerance (rtol 2e-2 / atol 2e-2), plus: every element within
+    ``max_ulp`` bf16 ulp of the oracle and at most ``frac`` of them differing."""
+    np.testing.assert_allclose(out, ref, rtol=2e-2, atol=2e-2)
+    d = _ulp_dist(out, ref)
+    assert d.max() <= max_ulp, f"max bf16 ulp distance {d.max()}"
+    assert (d > 0).mean() < frac, f"bf16 mismatch fraction {(d > 0).mean()}"
+
+
+@pytest.mark.parametrize("MNK", [(4224, 1536, 1536), (300, 200, 176), (256, 256, 128),
+                                 (17, 33, 16), (513, 1000, 272)])
+def test_fp8_gemm_vs_oracle(ops, MNK):
+    M, N, K = MNK
+    a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=M + N + K)
+    y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(sa).to(DEV), codes_dev(b),
+                     torch.from_numpy(sb).to(DEV), dev_bf16(bias))
+    ref = O.fp8_gemm(a, sa, b, sb, O.from_bf16_bits(bias))
+    _close_bf16(host_f(y), ref)
+
+
+def test_fp8_gemm_tensor_scales_and_golden(ops):
+    a = GOLD["gemm_a"].reshape(64, 256)
+    b = GOLD["gemm_b"].reshape(96, 256)
+    y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(GOLD["gemm_sa"]).to(DEV), codes_dev(b),
+                     torch.from_numpy(GOLD["gemm_sb"]).to(DEV), dev_bf16(GOLD["gemm_bias"]))
+    _close_bf16(host_f(y), O.from_bf16_bits(GOLD["gemm_out"]).reshape(64, 96))
+    a2, b2, _, _, _ = _gemm_inputs(128, 384, 512, seed=5)
+    sa, sb = np.float32([0.003]), np.float32([0.007])
+    y = ops.fp8_gemm(codes_dev(a2), torch.from_numpy(sa).to(DEV), codes_dev(b2),
+                     torch.from_numpy(sb).reshape(()).to(DEV))
+    _close_bf16(host_f(y), O.fp8_gemm(a2, sa, b2, sb))
+
+
+@pytest.mark.parametrize("MNK", [(1024, 8960, 1536), (300, 520, 256)])
+def test_gemm_gelu_epilogue_and_requant(ops, MNK):
+    from flashvsr_sm89_ops import _lib
+    M, N, K = MNK
+    a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=7 * M)
+    ad, bd = codes_dev(a), codes_dev(b)
+    sad, sbd = torch.from_numpy(sa).to(DEV), torch.from_numpy(sb).to(DEV)
+    h = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias))
+    nparts = (N + 127) // 128
+    amax = torch.empty((M, nparts), dtype=torch.float32, device=DEV)
+    g = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias), epilogue=_lib.EPI_GELU, amax_part=amax)
+    hb = host_bits(h)
+    gb = host_bits(g)
+    assert np.array_equal(gb, O.gelu_bf16(hb))  # GELU of the GEMM's own bf16 output, bitwise
+    gf = O.from_bf16_bits(gb)
+    am = host_f(amax)
+    for p in range(nparts):
+        assert np.array_equal(am[:, p], np.abs(gf[:, p * 128:(p + 1) * 128]).max(1))
+    from types import SimpleNamespace
+    from flashvsr_sm89_ops.fp8_ffn import gemm_gelu_quant_fp8
+    lin = SimpleNamespace(weight=bd, w_scale=sbd, bias=dev_bf16(bias))
+    for per_token in (True, False):
+        q, s = gemm_gelu_quant_fp8(ad, sad, lin, per_token)
+        rq, rs = O.quantize_fp8(hb, per_row=per_token, gelu=True)
+        assert np.array_equal(host_codes(q), rq)
+        assert np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_gemm_gate_add_epilogue(ops):
+    from flashvsr_sm89_ops import _lib
+    M, N, K = 600, 1536, 512
+    a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=3)
+    ad, bd = codes_dev(a), codes_dev(b)
+    sad, sbd = torch.from_numpy(sa).to(DEV), torch.from_numpy(sb).to(DEV)
+    res = rnd_bits((M, N), seed=4)
+    gate = rnd_bits((N,), seed=5, scale=0.5)
+    h = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias))
+    out = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias), epilogue=_lib.EPI_GATE_ADD,
+                       res=dev_bf16(res), gate=dev_bf16(gate))
+    ref = O.gate_add(O.from_bf16_bits(res), O.from_bf16_bits(gate)[None], host_f(h))
+    assert np.array_equal(host_bits(out), O.bf16_bits(ref))
+
+
+# ----------------------------------------------------------------------------- AdaLN
+
+@pytest.mark.parametrize("BLD", [(1, 16896, 1536), (2, 37, 1536), (2, 5, 100), (1, 3, 2048)])
+def test_ln_modulate(ops, BLD):
+    B, L, D = BLD
+    x = rnd_bits(BLD, seed=L)
+    sc = rnd_bits((B, 1, D), seed=L + 1, scale=0.1)
+    sh = rnd_bits((B, 1, D), seed=L + 2, scale=0.1)
+    xd, scd, shd = dev_bf16(x), dev_bf16(sc), dev_bf16(sh)
+    out = ops.fused_ln_modulate(xd, scd, shd, eps=1e-6)
+    ref = O.ln_modulate(O.from_bf16_bits(x), O.from_bf16_bits(sc), O.from_bf16_bits(sh), 1e-6)
+    _close_bf16(host_f(out), ref)
+    q, s, out2 = ops.fused_ln_modulate_quant(xd, scd, shd, eps=1e-6, write_bf16=True)
+    assert np.array_equal(host_bits(out2), host_bits(out))
+    rq, rs = O.quantize_fp8(host_bits(out).reshape(B * L, D), per_row=True)
+    assert np.array_equal(host_codes(q), rq)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+    q2, s2 = ops.fused_ln_modulate_quant(xd, scd, shd, eps=1e-6)
+    assert np.array_equal(host_codes(q2), rq)
+
+
+def test_ln_modulate_golden(ops):
+    out = ops.fused_ln_modulate(dev_bf16(GOLD["ln_x"].reshape(2, 16, 1536)),
+                                dev_bf16(GOLD["ln_scale"].reshape(2, 1, 1536)),
+                                dev_bf16(GOLD["ln_shift"].reshape(2, 1, 1536)))
+    _close_bf16(host_f(out), O.from_bf16_bits(GOLD["ln_out"]).reshape(2, 16, 1536))
+
+
+@pytest.mark.parametrize("BLD", [(1, 16896, 1536), (2, 7, 100), (3, 5, 1536)])
+def test_gate_add_bitwise(ops, BLD):
+    B, L, D = BLD
+    x, r = rnd_bits(BLD, seed=1), rnd_bits(BLD, seed=2)
+    g = rnd_bits((B, 1, D), seed=3, scale=0.5)
+    out = ops.fused_gate_add(dev_bf16(x), dev_bf16(g), dev_bf16(r))
+    ref = O.gate_add(O.from_bf16_bits(x), O.from_bf16_bits(g), O.from_bf16_bits(r))
+    assert np.array_equal(host_bits(out), O.bf16_bits(ref))
+
+
+def test_gate_add_golden(ops):
+    out = ops.fused_gate_add(dev_bf16(GOLD["ln_x"].reshape(2, 16, 1536)),
+                             dev_bf16(GOLD["ga_gate"].reshape(2, 1, 1536)),
+                             dev_bf16(GOLD["ga_res"].reshape(2, 16, 1536)))
+    assert np.array_equal(host_bits(out).reshape(-1), GOLD["ga_out"].reshape(-1))
+
+
+# ----------------------------------------------------------------------------- RMSNorm + RoPE
+
+def _rope_case(f, h, w, seed):
+    L, D = f * h * w, 1536
+    x = rnd_bits((1, L, D), seed=seed)
+    wt = O.bf16_bits((1 + 0.1 * np.random.default_rng(seed + 1).standard_normal(D)).astype(np.float32))
+    c, s = O.wan_rope_cos_sin(f, h, w)
+    return x, wt, c, s
+
+
+def _cs_dev(c, s):
+    return torch.from_numpy(np.stack([c, s], -1).astype(np.float32)).to(DEV)
+
+
+@pytest.mark.parametrize("fhw", [(2, 48, 88), (2, 4, 6)])
+def test_rms_rope(ops, fhw):
+    x, wt, c, s = _rope_case(*fhw, seed=fhw[1])
+    L = x.shape[1]
+    cs = _cs_dev(c, s)
+    freqs = torch.view_as_complex(cs)  # complex64 [L, 64]: the freqs_cis form
+    out = ops.fused_rms_rope(dev_bf16(x), dev_bf16(wt), freqs, eps=1e-6)
+    ref = O.rms_rope(O.from_bf16_bits(x), O.from_bf16_bits(wt), c, s, 1e-6)
+    _close_bf16(host_f(out), ref)
+    out_n = ops.fused_rms_rope(dev_bf16(x), dev_bf16(wt), None, rope=False)
+    _close_bf16(host_f(out_n), O.rms_rope(O.from_bf16_bits(x), O.from_bf16_bits(wt), rope=False))
+    # q/k fused launch equals two single launches, bitwise; in place on strided rows too
+    k = rnd_bits(x.shape, seed=5)
+    oq, ok = ops.fused_rms_rope_qk(dev_bf16(x), dev_bf16(k), dev_bf16(wt), dev_bf16(wt), freqs)
+    assert np.array_equal(host_bits(oq), host_bits(out))
+    ok1 = ops.fused_rms_rope(dev_bf16(k), dev_bf16(wt), freqs)
+    assert np.array_equal(host_bits(ok), host_bits(ok1))
+    qkv = torch.cat([dev_bf16(x)[0], dev_bf16(k)[0], dev_bf16(k)[0]], dim=1)
+    qv, kv = qkv[:, :1536].view(1, L, 1536), qkv[:, 1536:3072].view(1, L, 1536)
+    ops.fused_rms_rope_qk(qv, kv, dev_bf16(wt), dev_bf16(wt), freqs, inplace=True)
+    assert np.array_equal(host_bits(qkv[:, :1536]), host_bits(out)[0])
+    assert np.array_equal(host_bits(qkv[:, 1536:3072]), host_bits(ok1)[0])
+
+
+def test_rms_rope_golden_complex128_freqs(ops):
+    fr = torch.view_as_complex(torch.from_numpy(GOLD["rope_freqs"]).contiguous())  # complex128
+    out = ops.fused_rms_rope(dev_bf16(GOLD["rope_x"].reshape(1, 48, 1536)),
+                             dev_bf16(GOLD["rope_w"]), fr.to(DEV).reshape(48, 1, 64))
+    ref = O.from_bf16_bits(GOLD["rope_out"]).reshape(1, 48, 1536)
+    d = np.abs(host_f(out) - ref)
+    assert d.max() <= 0.03125 and (d > 1e-2).mean() < 1e-2
+
+
+# ----------------------------------------------------------------------------- attention
+
+def test_block_index_vs_oracle(ops):
+    keep = O.random_block_mask(3, 40, 150, 0.3, seed=3)
+    keep[1, 5] = False  # an empty row
+    sel, cnt, maxk = ops.build_csr(torch.from_numpy(keep).to(DEV))
+    rs, rc, _ = O.build_csr(keep)
+    sel, cnt = sel.cpu().numpy(), cnt.cpu().numpy()
+    assert np.array_equal(cnt, rc) and maxk == 150
+    for h in range(3):
+        for i in range(40):
+            assert np.array_equal(sel[h, i, :cnt[h, i]], rs[h, i, :cnt[h, i]])
+
+
+def _attn_check(out, ref, tol=1e-2):
+    err = np.abs(out - ref).max()
+    assert err <= tol, f"max abs err {err}"
+    return err
+
+
+def test_bsa_golden_dense_sdpa(ops):
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    q, k, v = (dev_bf16(GOLD[n]) for n in ("attn_q", "attn_k", "attn_v"))
+    q, k, v = q.view(256, 2, 128), k.view(384, 2, 128), v.view(384, 2, 128)
+    out = torch.empty_like(q)
+    block_sparse_attention_strided(q, k, v, torch.from_numpy(GOLD["attn_keep"]).to(DEV), None,
+                                   heads=2, head_dim=128, q_strides=(256, 128),
+                                   kv_strides=(256, 128), out=out)
+    _attn_check(host_f(out), GOLD["attn_out"])
+
+
+@pytest.mark.parametrize("case", [(16, 24, 0, 0.4), (32, 48, 0, 0.3), (48, 88, 198, 0.46)])
+def test_bsa_reference_cases(ops, case):
+    """The shapes of the reference's own test (lcsa/test_correctness.py:44-62),
+    masks from the draft top-k rule, inputs from a seeded numpy generator."""
+    h_lat, w_lat, nk_extra, ratio = case
+    H, D, f = 12, 128, 2
+    L = f * h_lat * w_lat
+    bh, bw = h_lat // 8, w_lat // 8
+    Nq = bh * bw
+    Nk = Nq + nk_extra
+    rng = np.random.default_rng(h_lat)
+    q = O.bf16(rng.standard_normal((L, H * D)).astype(np.float32))
+    k = O.bf16(rng.standard_normal((Nk * 128, H * D)).astype(np.float32))
+    v = O.bf16(rng.standard_normal((Nk * 128, H * D)).astype(np.float32))
+    qw = O.window_partition(q.reshape(1, f, h_lat, w_lat, H * D))
+    local = O.build_local_block_mask(bh, bw, 11)
+    keep = O.draft_block_mask(qw, k.reshape(Nk, 128, H * D), H, 1, local, int(Nq * Nk * ratio))
+    hs = list(range(H)) if Nk <= 100 else [0, 5, 11]  # oracle time: a few seconds
+    ref = O.sparse_attention(qw.reshape(-1, H, D)[:, hs], k.reshape(-1, H, D)[:, hs],
+                             v.reshape(-1, H, D)[:, hs], keep[hs])
+    out = ops.block_sparse_attention(dev_bf16(O.bf16_bits(qw.reshape(1, L, H * D))),
+                                     dev_bf16(O.bf16_bits(k[None])), dev_bf16(O.bf16_bits(v[None])),
+                                     torch.from_numpy(keep).to(DEV))
+    _attn_check(host_f(out).reshape(L, H, D)[:, hs], ref)
+
+
+def test_bsa_c4_full_size(ops):
+    """BASELINE C4: q,k,v [1,12,16896,128], 132x132 blocks, ~30% density."""
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_bhsd
+    H, S, D = 12, 16896, 128
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, H, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, H, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, H, S, D, generator=g).to(torch.bfloat16)
+    keep = O.c4_block_mask()
+    out = block_sparse_attention_bhsd(q.to(DEV), k.to(DEV), v.to(DEV), torch.from_numpy(keep).to(DEV))
+    qn, kn, vn = (t[0].float().numpy().transpose(1, 0, 2) for t in (q, k, v))
+    heads = [0, 7]  # two heads through the oracle keep the CPU time to seconds
+    ref = O.sparse_attention(qn[:, heads], kn[:, heads], vn[:, heads], keep[heads])
+    _attn_check(host_f(out)[0][heads].transpose(1, 0, 2), ref)
+
+
+def test_bsa_empty_rows_and_token_maps(ops):
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    H, D, NQ, NK = 2, 128, 3, 4
+    rng = np.random.default_rng(8)
+    q = O.bf16(rng.standard_normal((NQ * 128, H, D)).astype(np.float32))
+    k = O.bf16(rng.standard_normal((NK * 128, H, D)).astype(np.float32))
+    v = O.bf16(rng.standard_normal((NK * 128, H, D)).astype(np.float32))
+    keep = O.random_block_mask(H, NQ, NK, 0.5, seed=9)
+    keep[0, 1] = False
+    ref = O.sparse_attention(q, k, v, keep)
+    assert (ref[128:256, 0] == 0).all()
+    # store q/k/v permuted; the kernel reads them through the maps
+    pq, pk = rng.permutation(NQ * 128).astype(np.int32), rng.permutation(NK * 128).astype(np.int32)
+    qs, ks, vs = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    qs[pq], ks[pk], vs[pk] = q, k, v
+    out = torch.empty((NQ * 128, H, D), dtype=torch.bfloat16, device=DEV)
+    block_sparse_attention_strided(
+        dev_bf16(O.bf16_bits(qs)), dev_bf16(O.bf16_bits(ks)), dev_bf16(O.bf16_bits(vs)),
+        torch.from_numpy(keep).to(DEV), None, heads=H, head_dim=D, q_strides=(H * D, D),
+        kv_strides=(H * D, D), out=out, q_map=torch.from_numpy(pq).to(DEV),
+        kv_map=torch.from_numpy(pk).to(DEV))
+    got = host_f(out)[pq]
+    _attn_check(got, ref)
+    assert (got[128:256, 0] == 0).all()
+
+
+def test_compat_bsa_func(ops):
+    import block_sparse_attn
+    rng = np.random.default_rng(10)
+    H, D = 2, 128
+    q = O.bf16(rng.standard_normal((256, H, D)).astype(np.float32))
+    k = O.bf16(rng.standard_normal((384, H, D)).astype(np.float32))
+    v = O.bf16(rng.standard_normal((384, H, D)).astype(np.float32))
+    keep = O.random_block_mask(H, 2, 3, 0.6, seed=2)
+    out = block_sparse_attn.block_sparse_attn_func(
+        dev_bf16(O.bf16_bits(q)), dev_bf16(O.bf16_bits(k)), dev_bf16(O.bf16_bits(v)),
+        None, None, None, None, torch.from_numpy(keep[None]).to(DEV), 256, 384)
+    _attn_check(host_f(out), O.sparse_attention(q, k, v, keep))

@@ -1,0 +1,271 @@
+"""CPU tests of the host side: the C ABI library (load, exports, argument
+checks that run before any launch), the no-fallback rule, the
+``block_sparse_attn`` module injection and ``enable()``'s wiring logic.
+Nothing here launches a kernel."""
+import ctypes
+import os
+import re
+import sys
+import types
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fvsr.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fvsr_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from flashvsr_sm89_ops import _lib
+    return _lib.lib()
+
+
+def test_header_and_binding_agree():
+    from flashvsr_sm89_ops import _lib
+    assert declared_symbols() == sorted(_lib.exported_symbols())
+
+
+def test_library_exports_every_declared_symbol(L):
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+    out = os.popen(f"nm -D --defined-only {L._name}").read()
+    for name in declared_symbols():
+        assert re.search(rf"\bT {name}$", out, re.M), name
+
+
+def test_version(L):
+    assert L.fvsr_version().decode().startswith("fvsr ")
+
+
+def test_argument_checks_before_launch(L):
+    from flashvsr_sm89_ops import _lib
+    p = ctypes.c_void_p(16)  # never dereferenced: every call below fails its host checks
+    # GEMM: K must be a multiple of 16
+    assert L.fvsr_fp8_gemm(p, 17, p, 0, p, 17, p, 0, None, p, 8, 8, 8, 17, 0, None, None, None,
+                           None) == _lib.FVSR_EUNSUPPORTED
+    assert L.fvsr_fp8_gemm(p, 16, p, 0, p, 16, p, 0, None, p, 8, -1, 8, 16, 0, None, None, None,
+                           None) == _lib.FVSR_EINVAL
+    # GELU epilogue without its amax buffer
+    assert L.fvsr_fp8_gemm(p, 16, p, 0, p, 16, p, 0, None, p, 8, 8, 8, 16, 1, None, None, None,
+                           None) == _lib.FVSR_EINVAL
+    assert L.fvsr_fp8_gemm(p, 16, p, 0, p, 16, p, 0, None, p, 8, 8, 8, 16, 9, None, None, None,
+                           None) == _lib.FVSR_EINVAL
+    # empty problems are a no-op
+    assert L.fvsr_fp8_gemm(None, 16, None, 0, None, 16, None, 0, None, None, 8, 0, 8, 16, 0, None,
+                           None, None, None) == _lib.FVSR_OK
+    assert L.fvsr_quant_fp8(p, 4, 8, 8, 7, 0, p, p, p, 1, None) == _lib.FVSR_EINVAL
+    assert L.fvsr_quant_fp8(p, 4, 8, 4, 1, 0, p, p, p, 1, None) == _lib.FVSR_EINVAL  # ld < cols
+    assert L.fvsr_quant_fp8(p, 4, 8, 8, 0, 0, p, p, p, 0, None) == _lib.FVSR_EWORKSPACE
+    assert L.fvsr_quant_fp8(None, 0, 8, 8, 0, 0, None, None, None, 0, None) == _lib.FVSR_OK
+    assert L.fvsr_quant_workspace_floats(10_000, 1536, 0) == 1024
+    assert L.fvsr_quant_workspace_floats(3, 1536, 0) == 1
+    assert L.fvsr_gemm_amax_parts(8960) == 70
+    assert L.fvsr_bsa_fwd(p, p, p, p, 1536, 128, 1536, 128, 1536, 128, p, p, 4, 12, 4, 4, 64, 0.1,
+                          None, None, None) == _lib.FVSR_EUNSUPPORTED
+    assert L.fvsr_bsa_fwd(p, p, p, p, 1537, 128, 1536, 128, 1536, 128, p, p, 4, 12, 4, 4, 128, 0.1,
+                          None, None, None) == _lib.FVSR_EUNSUPPORTED
+    assert L.fvsr_rms_rope_qk(p, p, p, p, p, p, p, 1, 4, 1536, 128, 1e-6, 1000, 1536,
+                              None) == _lib.FVSR_EINVAL
+    assert L.fvsr_rms_rope(p, p, None, p, 1, 4, 1536, 128, 1e-6, 1, None) == _lib.FVSR_EINVAL
+    assert L.fvsr_ln_modulate(p, p, p, None, 1, 4, 1536, 1e-6, None, None, None) == _lib.FVSR_EINVAL
+    assert L.fvsr_block_index(None, 0, 4, 4, None, None, None) == _lib.FVSR_OK
+
+
+def test_no_cpu_fallback():
+    import flashvsr_sm89_ops as f
+    x = torch.zeros(4, 16, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        f.quantize_fp8(x)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        f.fused_gate_add(x[None], x[:1][None], x[None])
+    with pytest.raises(RuntimeError, match="GPU only"):
+        f.fused_rms_rope(x[None], x[0], None, rope=False)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    from flashvsr_sm89_ops import _lib
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.lib()
+
+
+# ----------------------------------------------------------------------------- compat_bsa
+
+def test_bsa_stub_modes(monkeypatch):
+    from flashvsr_sm89_ops import compat_bsa as cb
+    monkeypatch.delitem(sys.modules, "block_sparse_attn", raising=False)
+    monkeypatch.setenv("FS89_LCSA", "bsa")
+    assert cb.ensure_bsa_available() == "bsa"
+    assert "block_sparse_attn" not in sys.modules
+    assert cb.active_backend() == "bsa"
+    for mode in ("auto", "hip", "triton"):
+        monkeypatch.setenv("FS89_LCSA", mode)
+        monkeypatch.delitem(sys.modules, "block_sparse_attn", raising=False)
+        assert cb.active_backend() == "unresolved"
+        assert cb.ensure_bsa_available() == "hip"
+        mod = sys.modules["block_sparse_attn"]
+        assert mod.__version__ == cb.STUB_VERSION and cb.active_backend() == "hip"
+        assert callable(mod.block_sparse_attn_func)
+    other = types.ModuleType("block_sparse_attn")
+    other.__version__ = "2.0"
+    monkeypatch.setitem(sys.modules, "block_sparse_attn", other)
+    assert cb.active_backend() == "bsa"
+
+
+@pytest.mark.parametrize("kw", [dict(streaming_info=1), dict(is_causal=True),
+                                dict(dropout_p=0.1), dict(return_attn_probs=True)])
+def test_bsa_stub_rejects_unsupported(kw):
+    from flashvsr_sm89_ops.compat_bsa import _hip_block_sparse_attn_func
+    args = dict(q=None, k=None, v=None, cu_seqlens_q=None, cu_seqlens_k=None, head_mask_type=None,
+                streaming_info=None, attn_mask=None, max_seqlen_q=0, max_seqlen_k=0)
+    args.update(kw)
+    with pytest.raises(NotImplementedError):
+        _hip_block_sparse_attn_func(**args)
+
+
+# ----------------------------------------------------------------------------- integrate
+
+def make_fake_dit():
+    """A stand-in for diffsynth.models.wan_video_dit with the rebound classes,
+    stock helpers in torch, and the upstream forward signatures."""
+    dit = types.ModuleType("fake_wan_video_dit")
+
+    class SelfAttention(torch.nn.Module):
+        def forward(self, x, freqs, f=None, h=None, w=None, local_num=None, topk=None,
+                    train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                    is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+            raise AssertionError("stock forward must be rebound")
+
+    class CrossAttention(torch.nn.Module):
+        def forward(self, x, y, is_stream=False):
+            raise AssertionError
+
+    class DiTBlock(torch.nn.Module):
+        def __init__(self, dim=16):
+            super().__init__()
+            self.modulation = torch.nn.Parameter(torch.randn(1, 6, dim) * 0.1)
+            self.norm1 = torch.nn.LayerNorm(dim, eps=1e-6, elementwise_affine=False)
+            self.norm2 = torch.nn.LayerNorm(dim, eps=1e-6, elementwise_affine=False)
+            self.norm3 = torch.nn.LayerNorm(dim, eps=1e-6)
+
+        def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
+                    train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                    is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+            raise AssertionError
+
+        def gate(self, x, gate, residual):
+            return x + gate * residual
+
+    class WindowPartition3D:
+        @staticmethod
+        def partition(x, win):
+            raise NotImplementedError
+
+    dit.SelfAttention, dit.CrossAttention, dit.DiTBlock = SelfAttention, CrossAttention, DiTBlock
+    dit.WindowPartition3D = WindowPartition3D
+    dit.generate_draft_block_mask = lambda *a, **k: None
+    dit.modulate = lambda x, shift, scale: x * (1 + scale) + shift
+    return dit
+
+
+class FakePipe:
+    def __init__(self):
+        self.model = torch.nn.Module()
+
+    def denoising_model(self):
+        return self.model
+
+
+def test_drift_guard():
+    from flashvsr_sm89_ops.integrate import _check_dit_structure
+    dit = make_fake_dit()
+    _check_dit_structure(dit)
+    del dit.SelfAttention
+    with pytest.raises(RuntimeError, match="no SelfAttention"):
+        _check_dit_structure(dit)
+    dit = make_fake_dit()
+
+    class DiTBlock:
+        def forward(self, x, context):
+            pass
+    dit.DiTBlock = DiTBlock
+    with pytest.raises(RuntimeError, match="lacks args"):
+        _check_dit_structure(dit)
+    dit = make_fake_dit()
+    del dit.generate_draft_block_mask
+    with pytest.raises(RuntimeError, match="generate_draft_block_mask"):
+        _check_dit_structure(dit)
+
+
+def test_enable_wiring_flags_and_idempotence(monkeypatch, capsys):
+    import flashvsr_sm89_ops as f
+    from flashvsr_sm89_ops import integrate
+    dit = make_fake_dit()
+    stock = dit.SelfAttention.forward
+    monkeypatch.setenv("FS89_FP8", "")
+    applied = f.enable(FakePipe(), dit_module=dit)
+    assert applied == {"fused_rope": True, "fused_adaln": True, "lcsa_backend": "hip"}
+    assert dit.SelfAttention.forward is not stock and dit._FS89_PATCHED
+    assert dit.FUSED_ROPE_FN is f.fused_rms_rope
+    assert dit.FUSED_ADALN == (f.fused_ln_modulate, f.fused_gate_add)
+    assert "[flashvsr-mi355x-ops] enabled" in capsys.readouterr().out
+    rebound = dit.DiTBlock.forward
+    monkeypatch.setenv("FS89_FUSED_ROPE", "0")
+    monkeypatch.setenv("FS89_FUSED_ADALN", "0")
+    applied = f.enable(FakePipe(), dit_module=dit, verbose=False)
+    assert applied["fused_rope"] is False and dit.FUSED_ROPE_FN is None and dit.FUSED_ADALN is None
+    assert dit.DiTBlock.forward is rebound  # not rebound twice
+    with pytest.raises(ValueError):
+        f.enable(FakePipe(), dit_module=dit, scale_granularity="block")
+    monkeypatch.setitem(sys.modules, "diffsynth", None)
+    with pytest.raises(ImportError, match="wan_video_dit"):
+        integrate.enable(FakePipe())
+
+
+def test_stock_branch_dit_block_on_cpu(monkeypatch):
+    """With the fused flags off, the rebound DiTBlock.forward is the stock
+    math: AdaLN(shift, scale) order, gate, cross-attention residual."""
+    import flashvsr_sm89_ops as f
+    dit = make_fake_dit()
+    monkeypatch.setenv("FS89_FP8", "")
+    monkeypatch.setenv("FS89_FUSED_ROPE", "0")
+    monkeypatch.setenv("FS89_FUSED_ADALN", "0")
+    f.enable(FakePipe(), dit_module=dit, verbose=False)
+    blk = dit.DiTBlock(16)
+    seen = {}
+
+    def self_attn(x, *a, **k):
+        seen["attn_in"] = x
+        return x * 2, None, None
+    blk.self_attn = self_attn
+    blk.cross_attn = lambda x, ctx, is_stream=False: x * 0 + 1
+    blk.ffn = lambda x: x - 1
+    x = torch.randn(1, 5, 16)
+    t_mod = torch.randn(1, 6, 16) * 0.1
+    out = blk(x, None, t_mod, None, 1, 1, 5)
+    sh, sc, g, sh2, sc2, g2 = (blk.modulation + t_mod).chunk(6, dim=1)
+    ln = torch.nn.functional.layer_norm
+    a_in = ln(x, (16,), eps=1e-6) * (1 + sc) + sh
+    torch.testing.assert_close(seen["attn_in"], a_in)
+    x1 = x + g * (a_in * 2)
+    x1 = x1 + (ln(x1, (16,), weight=blk.norm3.weight, bias=blk.norm3.bias, eps=1e-6) * 0 + 1)
+    ref = x1 + g2 * ((ln(x1, (16,), eps=1e-6) * (1 + sc2) + sh2) - 1)
+    torch.testing.assert_close(out, ref)
+
+
+def test_window_token_map_matches_partition():
+    from flashvsr_sm89_ops.block import window_token_map
+    from oracle import oracle as O
+    f, h, w = 4, 16, 24
+    x = np.arange(f * h * w, dtype=np.float32).reshape(1, f, h, w, 1)
+    xw = O.window_partition(x).reshape(-1)
+    assert np.array_equal(window_token_map(f, h, w).numpy(), xw.astype(np.int32))
