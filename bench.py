@@ -1,0 +1,370 @@
+"""Benchmark of the MI355X FlashVSR DiT-block operator pack.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Workload (one "step"): BASELINE C5, one streaming chunk at the 1408x768
+FlashVSR-Tiny shape through the 30-block DiT stack: 16896 tokens
+(4 latent frames x 48 x 88), dim 1536, 12 heads x 128, FFN 8960,
+random-init weights ~N(0, 0.02) quantised to e4m3 per output channel,
+per-token activation scales, block-sparse attention with the C4 mask
+(~30% of the 132x132 block grid).  Inputs are resident in HBM before the
+timed region.  ``value`` is ms per DiT layer (block); lower is better.
+
+Alongside it the JSON line carries
+  roofline      the dominant kernel of the step, timed with HIP events on the
+                stream it runs on during the timed steps, against MI355X peak;
+  components    op-level measurements at the other BASELINE configs
+                (C1 FP8 linear, C2 RMSNorm+RoPE, C3 AdaLN + FP8 FFN, C4 BSA),
+                inputs rotated over > 512 MB so the 256 MB MALL cannot serve them;
+  cpu_baseline  the CPU oracle (numpy + C) running one DiT block of the same
+                workload on this machine's host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "flashvsr-sm89-ops_amd")]
+
+METRIC = "FP8 GEMM TFLOP/s, fused-op HBM GB/s, BSA ms/layer @1408×768; % roofline"
+PEAK = {"fp8": 5.0e15, "bf16": 2.5e15, "hbm": 8.0e12}
+F, H, W = 4, 48, 88            # latent frames x height x width at 1408x768
+L = F * H * W                  # 16896 tokens
+DIM, HEADS, HD, FFN = 1536, 12, 128, 8960
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class EventTimer:
+    """Events recorded on the current stream at hook points; durations by name."""
+
+    def __init__(self, torch, only=None):
+        self.torch, self.only = torch, only
+        self.marks = []
+
+    def __call__(self, name):
+        if self.only is not None and name != self.only and not (
+                self.marks and self.marks[-1][0] == self.only and self.marks[-1][2]):
+            return
+        ev = self.torch.cuda.Event(enable_timing=True)
+        ev.record()
+        self.marks.append((name, ev, name == self.only))
+
+    def durations(self):
+        out = {}
+        for (n0, e0, _), (n1, e1, _) in zip(self.marks, self.marks[1:]):
+            if self.only is not None and n0 != self.only:
+                continue
+            out.setdefault(n0, []).append(e0.elapsed_time(e1))
+        return out
+
+
+def block_costs():
+    """Algorithmic work per DiT block (per launch of each op)."""
+    gem = {
+        "gemm_qkv": 2 * L * DIM * 3 * DIM,
+        "gemm_o_gate": 2 * L * DIM * DIM,
+        "gemm_ffn0_gelu": 2 * L * DIM * FFN,
+        "gemm_ffn2_gate": 2 * L * FFN * DIM,
+    }
+    return gem
+
+
+def run_stack(args, torch, fv):
+    from flashvsr_sm89_ops.block import DiTStack, window_token_map
+    from flashvsr_sm89_ops.lcsa import build_csr
+    from flashvsr_sm89_ops.lcsa.masks import window_plus_random_mask
+    from flashvsr_sm89_ops.rope import wan_freqs_cis
+
+    dev = "cuda"
+    log(f"building {args.blocks}-block stack (random weights, e4m3 per channel)")
+    stack = DiTStack(args.blocks, DIM, HEADS, FFN, device=dev, seed=0)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(1, L, DIM, generator=g).to(torch.bfloat16).to(dev)
+    t_mod = (0.1 * torch.randn(1, 6, DIM, generator=g)).to(torch.bfloat16).to(dev)
+    cs = torch.view_as_real(wan_freqs_cis(F, H, W, HD).reshape(L, HD // 2)).to(dev)
+    keep = window_plus_random_mask(HEADS, 2, 6, 11, 7, 10, seed=7, device=dev)
+    kept = int(keep.sum().item())
+    index = build_csr(keep)
+    tmap = window_token_map(F, H, W, device=dev)
+    torch.cuda.synchronize()
+
+    # Per-op breakdown (untimed pass) to find the dominant kernel.
+    for _ in range(args.warmup):
+        y = stack(x, t_mod, cs, index, tmap)
+    torch.cuda.synchronize()
+    prof = EventTimer(torch)
+    stack(x, t_mod, cs, index, tmap, hook=prof)
+    torch.cuda.synchronize()
+    per_op = {k: sum(v) for k, v in prof.durations().items()}
+    dominant = max(per_op, key=per_op.get)
+    log("per-op ms per chunk: " + ", ".join(f"{k}={v:.3f}" for k, v in per_op.items()))
+
+    # Timed region: K steps; events only around the dominant kernel.
+    dom = EventTimer(torch, only=dominant)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    wall0 = time.perf_counter()
+    t0.record()
+    for _ in range(args.steps):
+        y = stack(x, t_mod, cs, index, tmap, hook=dom)
+    t1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    ms_step = t0.elapsed_time(t1) / args.steps
+    assert torch.isfinite(y.float()).all()
+    dom_ms = dom.durations()[dominant]
+    dom_avg = sum(dom_ms) / len(dom_ms)
+    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f}s); "
+        f"dominant {dominant}: {dom_avg:.4f} ms avg over {len(dom_ms)} launches")
+    return dict(ms_step=ms_step, per_op=per_op, dominant=dominant, dom_avg=dom_avg,
+                kept=kept, density=kept / (HEADS * 132 * 132))
+
+
+def roofline_for(name, avg_ms, kept):
+    costs = block_costs()
+    if name in costs:
+        ach = costs[name] / (avg_ms * 1e-3)
+        return {"kernel": name, "bound": "mfma", "achieved": ach / 1e12, "peak": PEAK["fp8"] / 1e12,
+                "unit": "TFLOP/s", "frac": ach / PEAK["fp8"],
+                "work_per_launch": f"{costs[name] / 1e9:.1f} GFLOP (2*M*N*K)"}
+    if name == "bsa":
+        fl = 4 * 128 ** 3 * kept
+        ach = fl / (avg_ms * 1e-3)
+        return {"kernel": name, "bound": "mfma", "achieved": ach / 1e12, "peak": PEAK["bf16"] / 1e12,
+                "unit": "TFLOP/s", "frac": ach / PEAK["bf16"],
+                "work_per_launch": f"{fl / 1e9:.1f} GFLOP (4*128^3 per kept block, {kept} blocks)"}
+    return {"kernel": name, "bound": "hbm", "achieved": None, "peak": PEAK["hbm"] / 1e9,
+            "unit": "GB/s", "frac": None}
+
+
+def timeit(torch, fn, n_sets, iters=20, warmup=3):
+    """Average ms per call, cycling through n_sets input sets."""
+    for i in range(warmup):
+        fn(i % n_sets)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(iters):
+        fn(i % n_sets)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def n_sets_for(bytes_per_set, target=640e6):
+    return max(2, int(math.ceil(target / bytes_per_set)))
+
+
+def components(torch, fv):
+    from flashvsr_sm89_ops.fp8_ffn import gemm_gelu_quant_fp8
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_bhsd
+    from flashvsr_sm89_ops.lcsa.masks import window_plus_random_mask
+    from flashvsr_sm89_ops.rope import wan_freqs_cis
+    from flashvsr_sm89_ops import _lib
+    from types import SimpleNamespace
+
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = {}
+
+    def randn(*s, std=1.0):
+        return (torch.randn(*s, generator=g, device=dev) * std).to(torch.bfloat16)
+
+    def gbs(nbytes, ms):
+        return nbytes / (ms * 1e-3) / 1e9
+
+    # C1: FP8 linear [4224,1536] x [1536,1536]^T, per-token x, per-channel W.
+    M, K, N = 4224, 1536, 1536
+    ns = n_sets_for(M * K * 2)
+    xs = [randn(M, K) for _ in range(ns)]
+    w8, ws = fv.quantize_weight_fp8(randn(N, K, std=0.02), per_channel=True)
+    bias = torch.zeros(N, dtype=torch.bfloat16, device=dev)
+    q = [fv.quantize_fp8(x, per_token=True) for x in xs]
+    t_q = timeit(torch, lambda i: fv.quantize_fp8(xs[i], per_token=True), ns)
+    t_g = timeit(torch, lambda i: fv.fp8_gemm(q[i][0], q[i][1], w8, ws, bias), ns)
+    qbytes = M * K * 3 + M * 4
+    out["C1_fp8_linear"] = {
+        "quant_ms": t_q, "quant_GBps": gbs(qbytes, t_q), "quant_frac_hbm": gbs(qbytes, t_q) * 1e9 / PEAK["hbm"],
+        "gemm_ms": t_g, "gemm_TFLOPs": 2 * M * N * K / (t_g * 1e-3) / 1e12,
+        "gemm_frac_fp8": 2 * M * N * K / (t_g * 1e-3) / PEAK["fp8"]}
+    del xs, q
+
+    # C2: RMSNorm + RoPE on q and k [1, 8448, 1536], Wan 3-D freqs (2, 48, 88).
+    L2 = 2 * 48 * 88
+    nbytes = 4 * L2 * DIM * 2 + 2 * DIM * 2 + L2 * 64 * 8
+    ns = n_sets_for(nbytes)
+    qs = [randn(1, L2, DIM) for _ in range(ns)]
+    ks = [randn(1, L2, DIM) for _ in range(ns)]
+    wq, wk = (1 + 0.1 * torch.randn(DIM, device=dev, generator=g)).to(torch.bfloat16), \
+        (1 + 0.1 * torch.randn(DIM, device=dev, generator=g)).to(torch.bfloat16)
+    fc = wan_freqs_cis(2, 48, 88, device=dev)
+    t = timeit(torch, lambda i: fv.fused_rms_rope_qk(qs[i], ks[i], wq, wk, fc), ns)
+    out["C2_rms_rope_qk"] = {"ms": t, "GBps": gbs(nbytes, t), "frac_hbm": gbs(nbytes, t) * 1e9 / PEAK["hbm"],
+                             "algorithmic_MB": nbytes / 1e6}
+    del qs, ks
+
+    # C3: AdaLN + FP8 FFN at M = 16896.
+    M3 = L
+    mod = (0.1 * torch.randn(1, 6, DIM, generator=g, device=dev)).to(torch.bfloat16)
+    sh, sc, gt = mod[:, 3:4].contiguous(), mod[:, 4:5].contiguous(), mod[:, 5:6].contiguous()
+    ns = n_sets_for(M3 * DIM * 2)
+    xs = [randn(1, M3, DIM) for _ in range(ns)]
+    t_ln = timeit(torch, lambda i: fv.fused_ln_modulate_quant(xs[i], sc, sh), ns)
+    ln_bytes = M3 * DIM * 3 + M3 * 4 + 2 * DIM * 2
+    t_lnb = timeit(torch, lambda i: fv.fused_ln_modulate(xs[i], sc, sh), ns)
+    lnb_bytes = M3 * DIM * 4 + 2 * DIM * 2
+    w1, s1 = fv.quantize_weight_fp8(randn(FFN, DIM, std=0.02), per_channel=True)
+    w2, s2 = fv.quantize_weight_fp8(randn(DIM, FFN, std=0.02), per_channel=True)
+    b1 = torch.zeros(FFN, dtype=torch.bfloat16, device=dev)
+    b2 = torch.zeros(DIM, dtype=torch.bfloat16, device=dev)
+    lin1 = SimpleNamespace(weight=w1, w_scale=s1, bias=b1)
+    x8s = [fv.fused_ln_modulate_quant(x, sc, sh) for x in xs[:2]]
+    nparts = (FFN + 127) // 128
+    amax = torch.empty((M3, nparts), dtype=torch.float32, device=dev)
+    t_g1 = timeit(torch, lambda i: fv.fp8_gemm(x8s[i % 2][0], x8s[i % 2][1], w1, s1, b1,
+                                               epilogue=_lib.EPI_GELU, amax_part=amax), 2)
+    h = fv.fp8_gemm(x8s[0][0], x8s[0][1], w1, s1, b1, epilogue=_lib.EPI_GELU, amax_part=amax)
+    from flashvsr_sm89_ops.fp8_quant import _workspace
+    hq = torch.empty((M3, FFN), dtype=torch.float8_e4m3fn, device=dev)
+    hsc = torch.empty((M3, 1), dtype=torch.float32, device=dev)
+    wsp = _workspace(h, M3, FFN, 1)
+
+    def requant(i):
+        _lib.lib().fvsr_quant_fp8_from_amax(h.data_ptr(), M3, FFN, amax.data_ptr(), nparts, 1,
+                                            hq.data_ptr(), hsc.data_ptr(), wsp.data_ptr(),
+                                            wsp.numel(), _lib.stream(h))
+    t_rq = timeit(torch, requant, 1)
+    rq_bytes = M3 * FFN * 3 + M3 * nparts * 4 + M3 * 4
+    res = xs[0].view(M3, DIM)
+    o2 = torch.empty((M3, DIM), dtype=torch.bfloat16, device=dev)
+    t_g2 = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2, epilogue=_lib.EPI_GATE_ADD,
+                                               res=res, gate=gt.view(DIM)), 1)
+    t_ga = timeit(torch, lambda i: fv.fused_gate_add(xs[i], gt, xs[(i + 1) % ns]), ns)
+    ga_bytes = M3 * DIM * 6 + DIM * 2
+    t_ffn = timeit(torch, lambda i: (lambda h8: fv.fp8_gemm(h8[0], h8[1], w2, s2, b2))(
+        gemm_gelu_quant_fp8(x8s[i % 2][0], x8s[i % 2][1], lin1, True)), 2)
+    fl = 2 * M3 * DIM * FFN
+    out["C3_adaln_fp8_ffn"] = {
+        "ln_modulate_quant_ms": t_ln, "ln_modulate_quant_GBps": gbs(ln_bytes, t_ln),
+        "ln_modulate_quant_frac_hbm": gbs(ln_bytes, t_ln) * 1e9 / PEAK["hbm"],
+        "ln_modulate_bf16_ms": t_lnb, "ln_modulate_bf16_GBps": gbs(lnb_bytes, t_lnb),
+        "gemm_ffn0_gelu_ms": t_g1, "gemm_ffn0_gelu_TFLOPs": fl / (t_g1 * 1e-3) / 1e12,
+        "gemm_ffn0_gelu_frac_fp8": fl / (t_g1 * 1e-3) / PEAK["fp8"],
+        "gelu_requant_ms": t_rq, "gelu_requant_GBps": gbs(rq_bytes, t_rq),
+        "gemm_ffn2_gate_ms": t_g2, "gemm_ffn2_gate_TFLOPs": fl / (t_g2 * 1e-3) / 1e12,
+        "gemm_ffn2_gate_frac_fp8": fl / (t_g2 * 1e-3) / PEAK["fp8"],
+        "gate_add_ms": t_ga, "gate_add_GBps": gbs(ga_bytes, t_ga),
+        "gate_add_frac_hbm": gbs(ga_bytes, t_ga) * 1e9 / PEAK["hbm"],
+        "ffn_chain_ms": t_ffn}
+    del xs, x8s, h, hq
+
+    # C4: block-sparse attention [1,12,16896,128], C4 mask, plus a density sweep.
+    qkv = [randn(1, HEADS, L, HD) for _ in range(3)]
+    keep = window_plus_random_mask(device=dev)
+    kept = int(keep.sum().item())
+    t4 = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkv, keep), 1, iters=10)
+    fl4 = 4 * 128 ** 3 * kept
+    sweep = []
+    from flashvsr_sm89_ops.lcsa.masks import density_mask
+    for d in (0.1, 0.2, 0.3, 0.5, 0.75, 1.0):
+        km = density_mask(HEADS, 132, 132, d, seed=11, device=dev)
+        kk = int(km.sum().item())
+        td = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkv, km), 1, iters=5)
+        sweep.append({"density": kk / (HEADS * 132 * 132), "ms": td,
+                      "TFLOPs": 4 * 128 ** 3 * kk / (td * 1e-3) / 1e12})
+    out["C4_bsa"] = {"ms_per_layer": t4, "density": kept / (HEADS * 132 * 132),
+                     "TFLOPs": fl4 / (t4 * 1e-3) / 1e12, "frac_bf16": fl4 / (t4 * 1e-3) / PEAK["bf16"],
+                     "density_sweep": sweep}
+    return out
+
+
+def cpu_baseline(args):
+    """One DiT block of the C5 workload through the CPU oracle (numpy + C)."""
+    import numpy as np
+    from oracle import oracle as O
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    rng = np.random.default_rng(0)
+    x = O.bf16(rng.standard_normal((L, DIM)).astype(np.float32))
+    mod = O.bf16((0.1 * rng.standard_normal((6, DIM))).astype(np.float32))
+
+    def lin(n, k):
+        w = O.bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+        q, s = O.quantize_weight(w, per_channel=True)
+        return q, s, np.zeros(n, np.float32)
+
+    params = {"q": lin(DIM, DIM), "k": lin(DIM, DIM), "v": lin(DIM, DIM), "o": lin(DIM, DIM),
+              "ffn0": lin(FFN, DIM), "ffn2": lin(DIM, FFN),
+              "norm_q": np.ones(DIM, np.float32), "norm_k": np.ones(DIM, np.float32)}
+    cos, sin = O.wan_rope_cos_sin(F, H, W)
+    keep = O.c4_block_mask()
+    t0 = time.perf_counter()
+    y = O.dit_block(x, mod, params, (F, H, W), keep, cos, sin, HEADS)
+    dt = time.perf_counter() - t0
+    assert np.isfinite(y).all()
+    return {"value": dt * 1e3, "unit": "ms/layer", "cores": threads, "kind": "port",
+            "sample": "1 of the 30 DiT blocks of the C5 chunk (16896 tokens), CPU oracle "
+                      "(numpy float64 GEMM accumulation + C quantisation), wall time"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--blocks", type=int, default=30)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-components", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this operator pack runs on one GPU; multi-GPU runs are not part of "
+              "this build (see DESIGN.md for how the path would shard).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import flashvsr_sm89_ops as fv
+    from flashvsr_sm89_ops import _lib
+
+    log(f"{_lib.version()} on {torch.cuda.get_device_name(0)}")
+    r = run_stack(args, torch, fv)
+    roof = roofline_for(r["dominant"], r["dom_avg"], r["kept"])
+    roof["traffic"] = load_traffic(r["dominant"])
+    comps = {} if args.no_components else components(torch, fv)
+    comps["C5_per_op_ms_per_chunk"] = r["per_op"]
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args)
+    ms_layer = r["ms_step"] / args.blocks
+    line = {
+        "metric": METRIC, "value": ms_layer, "unit": "ms/layer", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms_step"],
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "e4m3+bf16", "data": "synthetic",
+        "config": {"workload": f"C5: {args.blocks}-block FlashVSR-Tiny DiT stack, one chunk @1408x768",
+                   "tokens": L, "dim": DIM, "heads": HEADS, "head_dim": HD, "ffn": FFN,
+                   "blocks": args.blocks, "bsa_density": r["density"], "scales": "per-token x per-channel"},
+        "roofline": roof, "cpu_baseline": cpu, "components": comps,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def load_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC
+    summary (profiles/traffic.json), or None."""
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(p) as fh:
+            return json.load(fh).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+if __name__ == "__main__":
+    main()

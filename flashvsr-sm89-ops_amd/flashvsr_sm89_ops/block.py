@@ -27,7 +27,7 @@ import math
 import torch
 
 from . import _lib
-from .fp8_ffn import gemm_gelu_quant_fp8
+from .fp8_ffn import gemm_gelu, quantize_fp8_from_amax
 from .fp8_linear import FP8Linear, fp8_gemm
 from .fp8_quant import quantize_fp8, quantize_weight_fp8
 from .fused_adaln import fused_ln_modulate_quant
@@ -73,37 +73,53 @@ class _Lin:
 
 
 def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor, cs: torch.Tensor,
-                      index, tok_map: torch.Tensor, heads: int = 12, eps: float = 1e-6):
+                      index, tok_map: torch.Tensor, heads: int = 12, eps: float = 1e-6,
+                      hook=None):
     """x [1, L, dim] bf16 (raster order) -> [1, L, dim].  ``index`` is the
     device block index (sel, cnt, maxk) of the attention mask; ``tok_map``
-    is window_token_map(f, h, w); ``cs`` the (cos, sin) table [L, 64, 2]."""
+    is window_token_map(f, h, w); ``cs`` the (cos, sin) table [L, 64, 2].
+    ``hook(name)``, if given, is called on the host before each launch group
+    and with ``"end"`` after the last (used to place timing events)."""
+    mark = hook or (lambda name: None)
     B, L, D = x.shape
     hd = D // heads
     mod = (wts.modulation + t_mod).contiguous()
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = [
         mod[:, i:i + 1].contiguous() for i in range(6)]
 
+    mark("ln_modulate_quant")
     x8, xs = fused_ln_modulate_quant(x, scale_msa, shift_msa, eps)
+    mark("gemm_qkv")
     qkv = fp8_gemm(x8, xs, *wts.qkv)                      # [L, 3D]
     q = qkv[:, :D].view(B, L, D)
     k = qkv[:, D:2 * D].view(B, L, D)
+    mark("rms_rope_qk")
     fused_rms_rope_qk(q, k, wts.norm_q, wts.norm_k, cs, eps=eps, head_dim=hd, inplace=True)
 
     attn = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    mark("bsa")
     block_sparse_attention_strided(
         qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], None, 1.0 / math.sqrt(hd), heads=heads,
         head_dim=hd, q_strides=(3 * D, hd), kv_strides=(3 * D, hd), out=attn,
         o_strides=(D, hd), q_map=tok_map, kv_map=tok_map, index=index)
 
+    mark("quant_attn")
     a8, as_ = quantize_fp8(attn, per_token=True)
     x1 = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    mark("gemm_o_gate")
     fp8_gemm(a8, as_, *wts.o, out=x1, epilogue=_lib.EPI_GATE_ADD, res=x.view(L, D),
              gate=gate_msa.view(D))
 
+    mark("ln_modulate_quant")
     x8, xs = fused_ln_modulate_quant(x1.view(B, L, D), scale_mlp, shift_mlp, eps)
-    h8, hs = gemm_gelu_quant_fp8(x8, xs, _Lin(*wts.ffn0), per_token=True)
+    mark("gemm_ffn0_gelu")
+    g, amax = gemm_gelu(x8, xs, _Lin(*wts.ffn0))
+    mark("gelu_requant")
+    h8, hs = quantize_fp8_from_amax(g, amax, per_token=True)
     x2 = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
+    mark("gemm_ffn2_gate")
     fp8_gemm(h8, hs, *wts.ffn2, out=x2, epilogue=_lib.EPI_GATE_ADD, res=x1, gate=gate_mlp.view(D))
+    mark("end")
     return x2.view(B, L, D)
 
 
@@ -117,9 +133,9 @@ class DiTStack:
         self.heads = heads
         self.weights = [DiTBlockWeights(dim, ffn_dim, device, g) for _ in range(blocks)]
 
-    def __call__(self, x, t_mod, cs, index, tok_map):
+    def __call__(self, x, t_mod, cs, index, tok_map, hook=None):
         for w in self.weights:
-            x = dit_block_forward(x, w, t_mod, cs, index, tok_map, self.heads)
+            x = dit_block_forward(x, w, t_mod, cs, index, tok_map, self.heads, hook=hook)
         return x
 
 

@@ -41,25 +41,39 @@ def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
     return x8, s
 
 
-def gemm_gelu_quant_fp8(x8: torch.Tensor, s: torch.Tensor, lin: FP8Linear, per_token: bool):
-    """mm0 with the GELU epilogue, then the requantisation of its bf16 output:
-    returns (codes, scale) of quantize_fp8(gelu(bf16(x8 @ W.T * s * w_scale + b)))."""
+def gemm_gelu(x8: torch.Tensor, s: torch.Tensor, lin):
+    """mm0 with the GELU epilogue: returns (g, amax_part) with
+    g = bf16(gelu(bf16(x8 @ W.T * s * w_scale + b))) [M, N] and the |g| maxima
+    per (row, 128-column slab) [M, ceil(N/128)]."""
     M = x8.shape[0]
     N = lin.weight.shape[0]
     nparts = int(_lib.lib().fvsr_gemm_amax_parts(N))
     amax = torch.empty((M, nparts), dtype=torch.float32, device=x8.device)
     g = fp8_gemm(x8, s, lin.weight, lin.w_scale, lin.bias, epilogue=_lib.EPI_GELU,
                  amax_part=amax)
-    h8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x8.device)
-    hs = (torch.empty((M, 1), dtype=torch.float32, device=x8.device) if per_token
-          else torch.zeros(1, dtype=torch.float32, device=x8.device))
+    return g, amax
+
+
+def quantize_fp8_from_amax(g: torch.Tensor, amax: torch.Tensor, per_token: bool):
+    """e4m3 codes of g [M, N] bf16 whose |g| maxima are given per (row, slab)."""
+    M, N = g.shape
+    h8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=g.device)
+    hs = (torch.empty((M, 1), dtype=torch.float32, device=g.device) if per_token
+          else torch.zeros(1, dtype=torch.float32, device=g.device))
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
     ws = _workspace(g, M, N, mode)
-    _lib.check(_lib.lib().fvsr_quant_fp8_from_amax(g.data_ptr(), M, N, amax.data_ptr(), nparts,
-                                                   mode, h8.data_ptr(), hs.data_ptr(),
-                                                   ws.data_ptr(), ws.numel(), _lib.stream(g)),
-               "gelu requantisation")
+    _lib.check(_lib.lib().fvsr_quant_fp8_from_amax(g.data_ptr(), M, N, amax.data_ptr(),
+                                                   amax.shape[1], mode, h8.data_ptr(),
+                                                   hs.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                   _lib.stream(g)), "gelu requantisation")
     return h8, hs
+
+
+def gemm_gelu_quant_fp8(x8: torch.Tensor, s: torch.Tensor, lin, per_token: bool):
+    """mm0 with the GELU epilogue, then the requantisation of its bf16 output:
+    returns (codes, scale) of quantize_fp8(gelu(bf16(x8 @ W.T * s * w_scale + b)))."""
+    g, amax = gemm_gelu(x8, s, lin)
+    return quantize_fp8_from_amax(g, amax, per_token)
 
 
 class FP8FFN(nn.Module):
