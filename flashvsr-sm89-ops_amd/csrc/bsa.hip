@@ -127,6 +127,7 @@ FVSR_DEV void bsa_step(uint8_t LDS_AS* cur, uint8_t LDS_AS* nxt, int it, const S
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[jk][e]);
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c.scale_log2;
   if (__ballot(mx > m_run + 8.0f) != 0) {  // move the max (wave-uniform)
+    asm volatile("" :::);  // keep this a branch: the rescale is rare after the first steps
     const float m_new = fmaxf(m_run, mx);
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     m_run = m_new;

@@ -52,46 +52,49 @@ FVSR_DEV float wave_sum(float v) {
   return v;
 }
 
-// Shared fp32 exp: Cody-Waite reduction by ln2 split in two parts, degree-7
-// Taylor polynomial in Horner form, two exact power-of-two scalings.  Every
-// step is a single IEEE binary32 multiply or add (the translation units that
-// use it are compiled with contraction off), so the CPU oracle's C copy of the
-// same sequence returns identical bits.
-FVSR_DEV float fvsr_expf(float x) {
+// Shared fp32 exp for y clamped to [-40, 40] (the GELU below is saturated
+// outside): Cody-Waite reduction by ln2 in two fused steps, degree-6 Taylor
+// polynomial in fused Horner form, exact ldexp.  Every step is one IEEE
+// operation, so the CPU oracle's C copy of this sequence (fmaf, nearbyintf,
+// ldexpf) returns identical bits.
+FVSR_DEV float fvsr_expf(float y) {
+#pragma clang fp contract(off)
   const float LOG2E = 1.44269502162933349609375f;
   const float LN2_HI = 0.693145751953125f;
   const float LN2_LO = 1.428606765330187045e-06f;
-  if (x != x) return x;
-  if (x > 88.7228394f) return __builtin_huge_valf();
-  if (x < -103.972084f) return 0.0f;
-  float t = x * LOG2E;
-  float n = __builtin_rintf(t);
-  float r = x - n * LN2_HI;
-  r = r - n * LN2_LO;
-  float p = 1.984126984126984e-04f;
-  p = p * r + 1.388888888888889e-03f;
-  p = p * r + 8.333333333333333e-03f;
-  p = p * r + 4.166666666666666e-02f;
-  p = p * r + 1.666666666666667e-01f;
-  p = p * r + 0.5f;
-  p = p * r + 1.0f;
-  p = p * r + 1.0f;
-  int ni = (int)n;
-  int h = ni / 2;
-  float s1 = __uint_as_float((uint32_t)(h + 127) << 23);
-  float s2 = __uint_as_float((uint32_t)(ni - h + 127) << 23);
-  return (p * s1) * s2;
+  if (y != y) return y;
+  y = y < -40.0f ? -40.0f : (y > 40.0f ? 40.0f : y);
+  const float n = __builtin_rintf(y * LOG2E);
+  float r = __builtin_fmaf(-n, LN2_HI, y);
+  r = __builtin_fmaf(-n, LN2_LO, r);
+  float p = 1.388888888888889e-03f;
+  p = __builtin_fmaf(p, r, 8.333333333333333e-03f);
+  p = __builtin_fmaf(p, r, 4.166666666666666e-02f);
+  p = __builtin_fmaf(p, r, 1.666666666666667e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  return __builtin_ldexpf(p, (int)n);
 }
 
-// tanh-GELU via 1 - 2/(exp(2u)+1), rounded to bf16 (returned as fp32),
-// operation order of flashvsr_sm89_ops/fp8_ffn.py:26-30.
+// tanh-GELU in the form of flashvsr_sm89_ops/fp8_ffn.py:24-30, rounded to bf16
+// (returned as fp32): u = sqrt(2/pi)(x + 0.044715 x^3), t = 1 - 2/(exp(2u)+1),
+// g = bf16(0.5 x (1 + t)).  IEEE division.
 FVSR_DEV float gelu_tanh_bf16(float x) {
-  const float C0 = 0.7978845608028654f;
-  float u = C0 * (x + ((0.044715f * x) * x) * x);
-  float t = 1.0f - 2.0f / (fvsr_expf(2.0f * u) + 1.0f);
-  float g = (0.5f * x) * (1.0f + t);
-  return round_bf16(g);
+#pragma clang fp contract(off)
+  const float C2 = 1.5957691216057308f;  // 2*sqrt(2/pi)
+  const float x2 = x * x;
+  const float inner = __builtin_fmaf(0.044715f * x2, x, x);
+  const float e = fvsr_expf(C2 * inner);
+  const float t = 1.0f - 2.0f / (e + 1.0f);
+  return round_bf16((0.5f * x) * (1.0f + t));
 }
+
+// Largest |GELU| over negative inputs is 0.16992 (exhaustive over bf16), and
+// the bf16 GELU above is non-decreasing for x >= -0.75; so for a row whose
+// largest element is h_max, max|gelu(row)| == gelu(h_max) whenever that value
+// exceeds this bound.
+#define FVSR_GELU_NEG_BOUND 0.17f
 
 static inline int fvsr_launch_status() {
   hipError_t e = hipGetLastError();

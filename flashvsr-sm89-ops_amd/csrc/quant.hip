@@ -145,16 +145,19 @@ __global__ __launch_bounds__(kThreads) void amax_partial(
   if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
-// Max of n floats -> part[blockIdx.x] (used on GEMM-epilogue partial maxima).
-__global__ __launch_bounds__(kThreads) void max_reduce(const float* __restrict__ in, int64_t n,
-                                                       float* __restrict__ part) {
+// Signed max of n floats -> part[blockIdx.x] (maxima of h, which may be negative).
+__global__ __launch_bounds__(kThreads) void max_reduce_signed(const float* __restrict__ in,
+                                                              int64_t n, float* __restrict__ part) {
   __shared__ float red[kWaves];
-  float m = 0.0f;
+  float m = -__builtin_huge_valf();
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads)
     m = fmaxf(m, in[i]);
-  m = block_max(m, red);
-  if (threadIdx.x == 0) part[blockIdx.x] = m;
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    part[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
 FVSR_DEV float reduce_partials(const float* __restrict__ part, int nparts, float* red) {
@@ -192,32 +195,33 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
   }
 }
 
-// Row mode with the row amax given as nparts partial maxima per row.
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void quant_rows_from_amax(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, const float* __restrict__ apart,
-    int64_t nparts, uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  float m = 0.0f;
-  for (int64_t i = lane; i < nparts; i += 64) m = fmaxf(m, apart[row * nparts + i]);
-  const float amax = wave_max(m);
-  const float s = qscale(amax);
-  const uint16_t* xr = x + row * cols;
-  uint8_t* qr = codes + row * cols;
-  if (VEC) {
-    for (int64_t c = lane; c < (cols >> 3); c += 64) {
-      u32x4_t v = *(const u32x4_t*)(xr + c * 8);
-      *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s);
-    }
-  } else {
-    for (int64_t c = lane; c < cols; c += 64) {
-      float q = clamp448(bf2f(xr[c]) / s);
-      qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
-    }
+// Per-tensor GELU quantisation after a row-max GEMM epilogue.  Step 2: every
+// workgroup reduces the partial maxima of h to h_max; if gelu(h_max) exceeds
+// the largest |GELU| of a negative input it is the tensor's max|gelu| and the
+// workgroup just records it, otherwise it scans its rows (GELU evaluated).
+__global__ __launch_bounds__(kThreads) void gelu_amax_from_hmax(
+    const uint16_t* __restrict__ h, int64_t rows, int64_t cols, const float* __restrict__ hpart,
+    int nh, float* __restrict__ gpart) {
+  __shared__ float red[kWaves];
+  float hm = -__builtin_huge_valf();
+  for (int i = threadIdx.x; i < nh; i += kThreads) hm = fmaxf(hm, hpart[i]);
+  hm = wave_max(hm);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = hm;
+  __syncthreads();
+  hm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float a = gelu_tanh_bf16(hm);
+  if (a > FVSR_GELU_NEG_BOUND) {
+    if (threadIdx.x == 0) gpart[blockIdx.x] = a;
+    return;
   }
-  if (lane == 0) scale_out[row] = amax / 448.0f;
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  float m = 0.0f;
+  for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
+       row += (int64_t)gridDim.x * kWaves)
+    for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(gelu_tanh_bf16(bf2f(h[row * cols + c]))));
+  m = block_max(m, red);
+  if (threadIdx.x == 0) gpart[blockIdx.x] = m;
 }
 
 // ---------------------------------------------------------------------------
@@ -335,39 +339,31 @@ extern "C" int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t
               : launch_tensor<false>(xp, rows, cols, ld, qp, scale_out, workspace, st);
 }
 
-extern "C" int fvsr_quant_fp8_from_amax(const void* x, int64_t rows, int64_t cols,
-                                        const float* amax_part, int64_t nparts, int mode,
-                                        void* codes, float* scale_out, float* workspace,
-                                        int64_t workspace_floats, void* stream) {
-  if (rows < 0 || cols < 0 || nparts <= 0 ||
-      (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW))
-    return FVSR_EINVAL;
+extern "C" int fvsr_gelu_quant_fp8_tensor(const void* h, int64_t rows, int64_t cols,
+                                          const float* hmax_part, int64_t nparts, void* codes,
+                                          float* scale_out, float* workspace,
+                                          int64_t workspace_floats, void* stream) {
+  if (rows < 0 || cols < 0 || nparts <= 0) return FVSR_EINVAL;
   if (rows == 0 || cols == 0) return FVSR_OK;
-  if (!x || !codes || !scale_out || !amax_part) return FVSR_EINVAL;
-  hipStream_t st = (hipStream_t)stream;
-  const uint16_t* xp = (const uint16_t*)x;
-  uint8_t* qp = (uint8_t*)codes;
-  const bool vec = (cols % 8 == 0) && aligned16(x) && aligned16(codes);
-  if (mode == FVSR_SCALE_ROW) {
-    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
-    if (vec)
-      hipLaunchKernelGGL((quant_rows_from_amax<true>), grid, block, 0, st, xp, rows, cols,
-                         amax_part, nparts, qp, scale_out);
-    else
-      hipLaunchKernelGGL((quant_rows_from_amax<false>), grid, block, 0, st, xp, rows, cols,
-                         amax_part, nparts, qp, scale_out);
-    return fvsr_launch_status();
-  }
+  if (!h || !codes || !scale_out || !hmax_part) return FVSR_EINVAL;
   const int P = partial_blocks(rows);
-  if (!workspace || workspace_floats < P) return FVSR_EWORKSPACE;
-  hipLaunchKernelGGL(max_reduce, dim3(P), dim3(kThreads), 0, st, amax_part, rows * nparts,
-                     workspace);
+  if (!workspace || workspace_floats < 2 * P) return FVSR_EWORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* hp = (const uint16_t*)h;
+  uint8_t* qp = (uint8_t*)codes;
+  float* hpart = workspace;
+  float* gpart = workspace + P;
+  hipLaunchKernelGGL(max_reduce_signed, dim3(P), dim3(kThreads), 0, st, hmax_part, rows * nparts,
+                     hpart);
+  hipLaunchKernelGGL(gelu_amax_from_hmax, dim3(P), dim3(kThreads), 0, st, hp, rows, cols, hpart,
+                     P, gpart);
+  const bool vec = (cols % 8 == 0) && aligned16(h) && aligned16(codes);
   if (vec)
-    hipLaunchKernelGGL((quant_tensor<false, true>), dim3(P), dim3(kThreads), 0, st, xp, rows,
-                       cols, cols, workspace, P, qp, scale_out);
+    hipLaunchKernelGGL((quant_tensor<true, true>), dim3(P), dim3(kThreads), 0, st, hp, rows, cols,
+                       cols, gpart, P, qp, scale_out);
   else
-    hipLaunchKernelGGL((quant_tensor<false, false>), dim3(P), dim3(kThreads), 0, st, xp, rows,
-                       cols, cols, workspace, P, qp, scale_out);
+    hipLaunchKernelGGL((quant_tensor<true, false>), dim3(P), dim3(kThreads), 0, st, hp, rows,
+                       cols, cols, gpart, P, qp, scale_out);
   return fvsr_launch_status();
 }
 

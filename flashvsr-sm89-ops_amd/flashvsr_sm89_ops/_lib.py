@@ -18,7 +18,7 @@ LIB_PATH = os.environ.get("FVSR_LIB", os.path.join(_HERE, "libfvsr.so"))
 
 FVSR_OK, FVSR_EINVAL, FVSR_EHIP, FVSR_EUNSUPPORTED, FVSR_EWORKSPACE = 0, -1, -2, -3, -4
 SCALE_TENSOR, SCALE_ROW = 0, 1
-EPI_BIAS, EPI_GELU, EPI_GATE_ADD = 0, 1, 2
+EPI_BIAS, EPI_ROWMAX, EPI_GATE_ADD = 0, 1, 2
 
 _ERR = {
     FVSR_EINVAL: "invalid argument",
@@ -36,7 +36,7 @@ _SIGS = {
     "fvsr_version": ([], ctypes.c_char_p),
     "fvsr_quant_workspace_floats": ([_I64, _I64, _I], _I64),
     "fvsr_quant_fp8": ([_P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
-    "fvsr_quant_fp8_from_amax": ([_P, _I64, _I64, _P, _I64, _I, _P, _P, _P, _I64, _P], _I),
+    "fvsr_gelu_quant_fp8_tensor": ([_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P], _I),
     "fvsr_quant_weight_fp8": ([_P, _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
     "fvsr_fp8_gemm": ([_P, _I64, _P, _I, _P, _I64, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I,
                        _P, _P, _P, _P], _I),

@@ -12,8 +12,8 @@ for gfx950 instead of as a sequence of eager ops:
   per-token quant of the attention output
   o projection + gate_add                      (FP8 GEMM, gate_add epilogue)
   fused_ln_modulate + per-token quant
-  ffn.0 + bias + tanh-GELU                     (FP8 GEMM, GELU epilogue + row amax)
-  GELU requant                                 (1 pass)
+  ffn.0 + bias                                 (FP8 GEMM)
+  tanh-GELU + per-token quant                  (1 pass, row in registers)
   ffn.2 + gate_add                             (FP8 GEMM, gate_add epilogue)
 
 Cross-attention and ``norm3`` are not part of the BASELINE C5 block stack; the
@@ -27,7 +27,7 @@ import math
 import torch
 
 from . import _lib
-from .fp8_ffn import gemm_gelu, quantize_fp8_from_amax
+from .fp8_ffn import fused_gelu_quant_fp8
 from .fp8_linear import FP8Linear, fp8_gemm
 from .fp8_quant import quantize_fp8, quantize_weight_fp8
 from .fused_adaln import fused_ln_modulate_quant
@@ -63,13 +63,6 @@ class DiTBlockWeights:
         self.norm_q = (1 + 0.1 * torch.randn(dim, generator=generator)).to(torch.bfloat16).to(device)
         self.norm_k = (1 + 0.1 * torch.randn(dim, generator=generator)).to(torch.bfloat16).to(device)
         self.modulation = (0.1 * torch.randn(1, 6, dim, generator=generator)).to(torch.bfloat16).to(device)
-
-
-class _Lin:
-    """Adapter giving gemm_gelu_quant_fp8 the FP8Linear fields it reads."""
-
-    def __init__(self, q, s, b):
-        self.weight, self.w_scale, self.bias = q, s, b
 
 
 def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor, cs: torch.Tensor,
@@ -112,10 +105,10 @@ def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor
 
     mark("ln_modulate_quant")
     x8, xs = fused_ln_modulate_quant(x1.view(B, L, D), scale_mlp, shift_mlp, eps)
-    mark("gemm_ffn0_gelu")
-    g, amax = gemm_gelu(x8, xs, _Lin(*wts.ffn0))
-    mark("gelu_requant")
-    h8, hs = quantize_fp8_from_amax(g, amax, per_token=True)
+    mark("gemm_ffn0")
+    h = fp8_gemm(x8, xs, *wts.ffn0)
+    mark("gelu_quant")
+    h8, hs = fused_gelu_quant_fp8(h, per_token=True)
     x2 = torch.empty((L, D), dtype=torch.bfloat16, device=x.device)
     mark("gemm_ffn2_gate")
     fp8_gemm(h8, hs, *wts.ffn2, out=x2, epilogue=_lib.EPI_GATE_ADD, res=x1, gate=gate_mlp.view(D))

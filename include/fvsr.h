@@ -44,8 +44,8 @@ enum { FVSR_SCALE_TENSOR = 0, FVSR_SCALE_ROW = 1 };
 /* GEMM epilogues. */
 enum {
   FVSR_EPI_BIAS = 0,     /* C = bf16(acc*sa*sb + bias)                                  */
-  FVSR_EPI_GELU = 1,     /* C = bf16(gelu_tanh(bf16(acc*sa*sb + bias))), plus |C| maxima
-                            per (row, 128-column slab) into `amax_part`                  */
+  FVSR_EPI_ROWMAX = 1,   /* C = bf16(acc*sa*sb + bias), plus max(C) (signed) per
+                            (row, 128-column slab) into `amax_part`                      */
   FVSR_EPI_GATE_ADD = 2  /* C = bf16(res + bf16(gate[n] * bf16(acc*sa*sb + bias)))      */
 };
 
@@ -69,14 +69,20 @@ int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mo
                    void* stream);
 
 /*
- * Quantisation whose amax is already known as partial maxima: row r's amax is
- * max(amax_part[r*nparts + 0 .. nparts-1]) (FVSR_SCALE_ROW) or the max over
- * all rows*nparts entries (FVSR_SCALE_TENSOR).  Used after an FVSR_EPI_GELU
- * GEMM: together they carry fused_gelu_quant_fp8 (fp8_ffn.py:57-72).
+ * Per-tensor e4m3 quantisation of tanh-GELU(h), the FFN mid-section of FP8FFN
+ * (fp8_ffn.py:43-72,84-96) in the reference's per-tensor mode, after an
+ * FVSR_EPI_ROWMAX GEMM: h bf16 [rows, cols] contiguous, hmax_part float
+ * [rows*nparts] the GEMM's per-slab maxima of h.  GELU is non-decreasing above
+ * -0.75 and |GELU| < 0.17 below 0, so max|gelu(h)| is gelu(max h) whenever that
+ * exceeds 0.17 and GELU runs once per element (otherwise one extra scan finds
+ * the maximum).  Same codes and scale as fvsr_quant_fp8(h, gelu = 1, mode =
+ * FVSR_SCALE_TENSOR).  workspace: 2 * fvsr_quant_workspace_floats(rows, cols, 0).
+ * (Per-row mode needs no helper: fvsr_quant_fp8(gelu = 1, FVSR_SCALE_ROW) keeps
+ * each row in registers and evaluates GELU once per element.)
  */
-int fvsr_quant_fp8_from_amax(const void* x, int64_t rows, int64_t cols, const float* amax_part,
-                             int64_t nparts, int mode, void* codes, float* scale_out,
-                             float* workspace, int64_t workspace_floats, void* stream);
+int fvsr_gelu_quant_fp8_tensor(const void* h, int64_t rows, int64_t cols, const float* hmax_part,
+                               int64_t nparts, void* codes, float* scale_out, float* workspace,
+                               int64_t workspace_floats, void* stream);
 
 /*
  * Static weight quantisation, reference FP8Linear.__init__
@@ -97,7 +103,7 @@ int fvsr_quant_weight_fp8(const void* w, int64_t n, int64_t k, int mode, void* c
  * FP8Linear._mm (fp8_linear.py:28-30).  sa: [1] or [M] (sa_mode), sb: [1] or
  * [N] (sb_mode).  bias: bf16 [N] or NULL.  C: bf16 [M,N] row stride ldc.
  * K must be a multiple of 16 and lda/ldb multiples of 16.
- * epilogue FVSR_EPI_GELU also needs amax_part (float [M, ceil(N/128)]);
+ * epilogue FVSR_EPI_ROWMAX also needs amax_part (float [M, ceil(N/128)]);
  * FVSR_EPI_GATE_ADD needs res (bf16 [M,N], row stride ldc) and gate (bf16 [N]).
  */
 int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa_mode,
@@ -106,7 +112,7 @@ int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa_mode,
                   int epilogue, float* amax_part, const void* res, const void* gate,
                   void* stream);
 
-/* Number of 128-column slabs FVSR_EPI_GELU writes per row: ceil(N/128). */
+/* Number of 128-column slabs FVSR_EPI_ROWMAX writes per row: ceil(N/128). */
 int64_t fvsr_gemm_amax_parts(int64_t N);
 
 /*

@@ -18,11 +18,12 @@
  *                     (fp8_quant.py:16-35,42-55), per tensor or per row.
  *   orc_gelu_bf16     tanh-GELU through 1-2/(exp(2u)+1), rounded to bf16
  *                     (fp8_ffn.py:24-30), with orc_expf as the exp.
- *   orc_expf          fp32 exp by Cody-Waite reduction + degree-7 Taylor
+ *   orc_expf          fp32 exp by Cody-Waite reduction + degree-6 Taylor
  *                     polynomial (W. J. Cody, W. Waite, "Software Manual for
- *                     the Elementary Functions", 1980), mul/add only.  The HIP
- *                     kernels run the same operation sequence, so the GELU
- *                     values (and therefore the FP8 codes) are bit-identical.
+ *                     the Elementary Functions", 1980), fused multiply-adds and
+ *                     an exact ldexp.  The HIP kernels run the same operation
+ *                     sequence, so the GELU values (and therefore the FP8
+ *                     codes) are bit-identical.
  *   orc_quant_weight  contract Q-W: per-tensor (fp8_linear.py:17-22, with the
  *                     bf16 intermediate roundings of eager type promotion) and
  *                     per-output-channel (fp32 division, single rounding).
@@ -79,43 +80,42 @@ void orc_bf16_round(const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = bf16r(x[i]);
 }
 
-/* exp(x) in binary32: n = rint(x*log2e); r = (x - n*ln2_hi) - n*ln2_lo;
- * p = Taylor_7(r) in Horner form; result = p * 2^n (two exact power-of-two
- * multiplies so 2^n never overflows the exponent field on its own). */
-float orc_expf(float x) {
+/* exp(y) for y clamped to [-40, 40]; the GELU below is already saturated
+ * there (1 + exp(-40) == 1 and 2/(exp(40)+1) < 2^-25, so 1 - 2/(e+1) is
+ * exactly -1 or 1 either way):  n = rint(y*log2e);  r = y - n*ln2 in two
+ * fused steps (Cody & Waite 1980);  p = degree-6 Taylor polynomial of e^r in
+ * fused Horner form;  result = ldexp(p, n), exact because the result is a
+ * normal number.  Every step is one IEEE operation (fmaf is a single rounding),
+ * so the device copy of this sequence returns identical bits. */
+float orc_expf(float y) {
     const float LOG2E = 1.44269502162933349609375f;
-    const float LN2_HI = 0.693145751953125f;          /* 11 significant bits: n*LN2_HI exact */
+    const float LN2_HI = 0.693145751953125f;
     const float LN2_LO = 1.428606765330187045e-06f;
-    if (x != x) return x;
-    if (x > 88.7228394f) return INFINITY;
-    if (x < -103.972084f) return 0.0f;
-    float t = x * LOG2E;
-    float n = nearbyintf(t);
-    float r = x - n * LN2_HI;
-    r = r - n * LN2_LO;
-    float p = 1.984126984126984e-04f;                 /* 1/7! */
-    p = p * r + 1.388888888888889e-03f;               /* 1/6! */
-    p = p * r + 8.333333333333333e-03f;               /* 1/5! */
-    p = p * r + 4.166666666666666e-02f;               /* 1/4! */
-    p = p * r + 1.666666666666667e-01f;               /* 1/3! */
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
-    int ni = (int)n;
-    int h = ni / 2;
-    float s1 = u2f((uint32_t)(h + 127) << 23);
-    float s2 = u2f((uint32_t)(ni - h + 127) << 23);
-    return (p * s1) * s2;
+    if (y != y) return y;
+    y = y < -40.0f ? -40.0f : (y > 40.0f ? 40.0f : y);
+    float n = nearbyintf(y * LOG2E);
+    float r = fmaf(-n, LN2_HI, y);
+    r = fmaf(-n, LN2_LO, r);
+    float p = 1.388888888888889e-03f;                 /* 1/6! */
+    p = fmaf(p, r, 8.333333333333333e-03f);          /* 1/5! */
+    p = fmaf(p, r, 4.166666666666666e-02f);          /* 1/4! */
+    p = fmaf(p, r, 1.666666666666667e-01f);          /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
 }
 
-/* tanh-GELU of one bf16-valued input, result rounded to bf16 (as fp32).
- * Operation order follows fp8_ffn.py:26-30 left to right. */
+/* tanh-GELU of one bf16-valued input, rounded to bf16 (as fp32), in the form
+ * of fp8_ffn.py:24-30:  u = sqrt(2/pi) (x + 0.044715 x^3),
+ * t = 1 - 2/(exp(2u) + 1) (= tanh u),  g = bf16(0.5 x (1 + t)). */
 float orc_gelu_one(float x) {
-    const float C0 = 0.7978845608028654f;
-    float u = C0 * (x + ((0.044715f * x) * x) * x);
-    float t = 1.0f - 2.0f / (orc_expf(2.0f * u) + 1.0f);
-    float g = (0.5f * x) * (1.0f + t);
-    return bf16r(g);
+    const float C2 = 1.5957691216057308f;             /* 2*sqrt(2/pi) */
+    float x2 = x * x;
+    float inner = fmaf(0.044715f * x2, x, x);         /* x + 0.044715 x^3 */
+    float e = orc_expf(C2 * inner);                   /* exp(2u) */
+    float t = 1.0f - 2.0f / (e + 1.0f);
+    return bf16r((0.5f * x) * (1.0f + t));
 }
 
 void orc_gelu_bf16(const uint16_t* h, uint16_t* g, int64_t n) {

@@ -195,32 +195,64 @@ def test_fp8_gemm_tensor_scales_and_golden(ops):
     _close_bf16(host_f(y), O.fp8_gemm(a2, sa, b2, sb))
 
 
-@pytest.mark.parametrize("MNK", [(1024, 8960, 1536), (300, 520, 256)])
-def test_gemm_gelu_epilogue_and_requant(ops, MNK):
+@pytest.mark.parametrize("MNK", [(1024, 8960, 1536), (300, 520, 256), (130, 200, 176)])
+def test_gemm_rowmax_epilogue_and_gelu_requant(ops, MNK):
+    """ROWMAX epilogue: same C as BIAS plus exact per-slab row maxima; the FFN
+    requantisation (per token and per tensor) is bit-exact with
+    quantize(gelu(h)) of the GEMM's own bf16 output."""
+    from types import SimpleNamespace
     from flashvsr_sm89_ops import _lib
+    from flashvsr_sm89_ops.fp8_ffn import gemm_gelu_quant_fp8
     M, N, K = MNK
     a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=7 * M)
     ad, bd = codes_dev(a), codes_dev(b)
     sad, sbd = torch.from_numpy(sa).to(DEV), torch.from_numpy(sb).to(DEV)
     h = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias))
     nparts = (N + 127) // 128
-    amax = torch.empty((M, nparts), dtype=torch.float32, device=DEV)
-    g = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias), epilogue=_lib.EPI_GELU, amax_part=amax)
+    hmax = torch.empty((M, nparts), dtype=torch.float32, device=DEV)
+    h2 = ops.fp8_gemm(ad, sad, bd, sbd, dev_bf16(bias), epilogue=_lib.EPI_ROWMAX, amax_part=hmax)
     hb = host_bits(h)
-    gb = host_bits(g)
-    assert np.array_equal(gb, O.gelu_bf16(hb))  # GELU of the GEMM's own bf16 output, bitwise
-    gf = O.from_bf16_bits(gb)
-    am = host_f(amax)
+    assert np.array_equal(host_bits(h2), hb)
+    hf = O.from_bf16_bits(hb)
+    hm = host_f(hmax)
     for p in range(nparts):
-        assert np.array_equal(am[:, p], np.abs(gf[:, p * 128:(p + 1) * 128]).max(1))
-    from types import SimpleNamespace
-    from flashvsr_sm89_ops.fp8_ffn import gemm_gelu_quant_fp8
+        assert np.array_equal(hm[:, p], hf[:, p * 128:(p + 1) * 128].max(1))
     lin = SimpleNamespace(weight=bd, w_scale=sbd, bias=dev_bf16(bias))
     for per_token in (True, False):
         q, s = gemm_gelu_quant_fp8(ad, sad, lin, per_token)
         rq, rs = O.quantize_fp8(hb, per_row=per_token, gelu=True)
         assert np.array_equal(host_codes(q), rq)
         assert np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_gelu_tensor_quant_small_values(ops):
+    """Per-tensor GELU requant when gelu(max h) is below the negative-branch
+    bound: the scan path must find the true max|gelu|."""
+    from flashvsr_sm89_ops import _lib
+    rng = np.random.default_rng(12)
+    h = O.bf16_bits((-0.75 - 2.0 * rng.random((37, 256))).astype(np.float32))  # all negative
+    hd = dev_bf16(h)
+    hmax = torch.from_numpy(O.from_bf16_bits(h).reshape(37, 2, 128).max(2)).contiguous().to(DEV)
+    q = torch.empty((37, 256), dtype=torch.float8_e4m3fn, device=DEV)
+    s = torch.zeros(1, dtype=torch.float32, device=DEV)
+    ws = torch.empty(2 * int(_lib.lib().fvsr_quant_workspace_floats(37, 256, 0)), device=DEV)
+    _lib.check(_lib.lib().fvsr_gelu_quant_fp8_tensor(hd.data_ptr(), 37, 256, hmax.data_ptr(), 2,
+                                                     q.data_ptr(), s.data_ptr(), ws.data_ptr(),
+                                                     ws.numel(), _lib.stream(hd)), "gelu tensor")
+    rq, rs = O.quantize_fp8(h, per_row=False, gelu=True)
+    assert np.array_equal(host_codes(q), rq) and np.array_equal(host_f(s), rs)
+
+
+@pytest.mark.parametrize("MNK", [(256, 256, 64), (300, 520, 192), (4224, 1536, 1536),
+                                 (1000, 600, 8960), (64, 64, 320)])
+def test_fp8_gemm_ring_shapes(ops, MNK):
+    """The direct-to-LDS ring main loop (K a multiple of 64) across K-step
+    counts that exercise the unroll-by-four tail and ragged M, N."""
+    M, N, K = MNK
+    a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=M * 3 + K)
+    y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(sa).to(DEV), codes_dev(b),
+                     torch.from_numpy(sb).to(DEV), dev_bf16(bias))
+    _close_bf16(host_f(y), O.fp8_gemm(a, sa, b, sb, O.from_bf16_bits(bias)))
 
 
 def test_gemm_gate_add_epilogue(ops):

@@ -70,13 +70,28 @@ def test_bf16_round_matches_torch():
 # ----------------------------------------------------------------------------- exp / GELU
 
 def test_shared_expf_accuracy():
-    xs = np.concatenate([np.linspace(-100, 88, 20001), np.linspace(-1, 1, 2001)]).astype(np.float32)
+    """Cody-Waite exp on its domain [-40, 40]: within 5 ulp of float64 exp
+    (measured 3.7); clamped outside."""
+    xs = np.concatenate([np.linspace(-40, 40, 40001), np.linspace(-1, 1, 2001)]).astype(np.float32)
     e = np.array([O.expf(float(v)) for v in xs], np.float64)
     ref = np.exp(xs.astype(np.float64))
-    keep = ref > 1.2e-38  # normal range
-    rel = np.abs(e[keep] - ref[keep]) / ref[keep]
-    assert rel.max() < 4 * 2.0**-24  # within 4 ulp (measured 1.6)
-    assert O.expf(0.0) == 1.0 and O.expf(1000.0) == math.inf and O.expf(-1000.0) == 0.0
+    rel = np.abs(e - ref) / ref
+    assert rel.max() < 5 * 2.0**-24
+    assert O.expf(0.0) == 1.0
+    assert O.expf(1000.0) == O.expf(40.0) and O.expf(-1000.0) == O.expf(-40.0)
+
+
+def test_gelu_rowmax_shortcut_preconditions():
+    """What the per-tensor GELU requantisation relies on, checked over every
+    finite bf16 input: GELU is non-decreasing for x >= -0.75 and |GELU(x)| < 0.17
+    for x < 0."""
+    x = O.from_bf16_bits(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+    x = x[np.isfinite(x)]
+    pos = np.sort(x[x >= -0.75])
+    g = O.from_bf16_bits(O.gelu_bf16(O.bf16_bits(pos)))
+    assert np.all(np.diff(g) >= 0)
+    neg = x[x < 0]
+    assert np.abs(O.from_bf16_bits(O.gelu_bf16(O.bf16_bits(neg)))).max() < 0.17
 
 
 def test_gelu_against_torch_all_bf16():
