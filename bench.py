@@ -314,10 +314,19 @@ def main():
     ap.add_argument("--blocks", type=int, default=30)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-components", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a float32 negation over this many MiB (read + write), the "
+                         "known-size kernel that calibrates FETCH_SIZE / WRITE_SIZE counters")
+    ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two rocprofv3 --pmc counter_collection.csv files "
+                         "(FETCH_SIZE, WRITE_SIZE) of a --copy-probe-mib run into JSON and exit")
     args = ap.parse_args()
+    if args.traffic_from:
+        print(json.dumps(summarize_traffic(*args.traffic_from, args.copy_probe_mib), indent=1))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this operator pack runs on one GPU; multi-GPU runs are not part of "
-              "this build (see DESIGN.md for how the path would shard).", file=sys.stderr)
+              "this build (the row-local ops shard by tokens, attention by heads).", file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -325,6 +334,14 @@ def main():
     from flashvsr_sm89_ops import _lib
 
     log(f"{_lib.version()} on {torch.cuda.get_device_name(0)}")
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     r = run_stack(args, torch, fv)
     roof = roofline_for(r["dominant"], r["dom_avg"], r["kept"])
     roof["traffic"] = load_traffic(r["dominant"])
@@ -345,15 +362,63 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def load_traffic(kernel):
-    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 PMC
-    summary (profiles/traffic.json), or None."""
+# Kernel (name fragment, grid size in work-items) of each op of the C5 stack,
+# for finding its dispatches in a counter file.  gemm_o_gate and
+# gemm_ffn2_gate share kernel and grid, so neither can be told apart there.
+OP_KERNELS = {
+    "bsa": ("bsa_fwd_kernel<true>", None),
+    "gemm_qkv": ("gemm_fp8_ring<0>", 66 * 18 * 256),
+    "gemm_ffn0": ("gemm_fp8_ring<0>", 66 * 35 * 256),
+}
+
+
+def summarize_traffic(fetch_csv, write_csv, copy_mib):
+    """HBM bytes per dispatch from two rocprofv3 --pmc runs of
+    ``bench.py --copy-probe-mib N --blocks 1 ...``: FETCH_SIZE and WRITE_SIZE
+    (KiB per dispatch) averaged per kernel and scaled by the factor that makes
+    the probe's negation over N MiB read and write exactly N MiB."""
+    import csv
+
+    def per_kernel(path, counter):
+        acc = {}
+        with open(path) as fh:
+            for row in csv.DictReader(fh):
+                if row["Counter_Name"] != counter:
+                    continue
+                key = (row["Kernel_Name"], int(row.get("Grid_Size") or 0))
+                d = acc.setdefault(key, {})
+                d[row["Dispatch_Id"]] = d.get(row["Dispatch_Id"], 0.0) + float(row["Counter_Value"])
+        return {k: sum(v.values()) / len(v) for k, v in acc.items()}
+
+    fetch, write = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    probe = [k for k in fetch if "neg" in k[0].lower()]
+    if not probe or copy_mib <= 0:
+        raise SystemExit("no calibration kernel (run with --copy-probe-mib)")
+    want = copy_mib * 1024.0
+    f_fac = want / (sum(fetch[k] for k in probe) / len(probe))
+    w_fac = want / (sum(write[k] for k in probe) / len(probe))
+    out = {"calibration": {"kernel": probe[0][0][:120], "bytes": copy_mib << 20,
+                           "fetch_factor": f_fac, "write_factor": w_fac}}
+    for op, (frag, grid) in OP_KERNELS.items():
+        keys = [k for k in fetch if frag in k[0] and (grid is None or k[1] == grid)]
+        if len(keys) != 1 or keys[0] not in write:
+            continue
+        fb, wb = fetch[keys[0]] * 1024 * f_fac, write[keys[0]] * 1024 * w_fac
+        out[op] = {"kernel": keys[0][0][:120], "fetch_bytes": fb, "write_bytes": wb,
+                   "traffic": fb + wb}
+    return out
+
+
+def load_traffic(op):
+    """HBM bytes per launch of ``op``'s kernel from the committed rocprofv3
+    counter summary (profiles/traffic.json), or None."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(p) as fh:
-            return json.load(fh).get(kernel)
+            ent = json.load(fh).get(op)
     except (OSError, ValueError):
         return None
+    return None if ent is None else ent["traffic"]
 
 
 if __name__ == "__main__":

@@ -4,7 +4,7 @@
  * One shared library, libfvsr.so, built from the HIP sources in
  * flashvsr-sm89-ops_amd/csrc.
  * The Python package flashvsr_sm89_ops binds these entry points with ctypes;
- * any other host language can bind them the same way (see INTEGRATION.md).
+ * any other host language can bind them the same way.
  *
  * Conventions shared by every entry point:
  *  - Tensors are raw device pointers.  bf16 tensors hold uint16 bit patterns,
