@@ -30,6 +30,13 @@
 // robin over the 8 XCDs) walks a contiguous, M-grouped range of tiles.
 #include "common.h"
 
+// Buffer loads straight into LDS (buffer_load_dwordx4 ... lds): the 16 bytes
+// at base + voffset + soffset of every lane land at M0 + 16 * lane.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ void fvsr_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds,
+                                     int size, int voffset, int soffset, int offset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.lds");
+
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -52,6 +59,7 @@ struct EpiArgs {
   const uint16_t* res;
   const uint16_t* gate;
   int sa_row, sb_col;
+  int vec_params;  // sb (per column) 16-byte aligned and bias 8-byte aligned
 };
 
 FVSR_DEV void map_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -197,138 +205,406 @@ FVSR_DEV void epilogue(const v16f (&acc)[4][4], const CTile& ct, int64_t m0, int
 }
 
 // ---------------------------------------------------------------------------
-// Main loop, K % 64 == 0: direct-to-LDS ring.
+// Main loop, K % 64 == 0 and K >= 256: persistent direct-to-LDS ring.
 // ---------------------------------------------------------------------------
-FVSR_DEV int swz64(int r, int c) { return c ^ ((r >> 2) & 3); }
+// The ring holds K in pairs of 64-byte steps: a pair slot keeps 128 bytes of
+// every A row and B row (64 KB), so each load covers whole 128-byte lines.
+// 16-byte chunk c of row r sits at chunk position c ^ (r & 7) ^ ((r >> 3) & 1):
+// any 8 consecutive rows read at one logical chunk hit 8 distinct 16-byte
+// bank groups, and any 16 consecutive rows 16 distinct (row parity, chunk)
+// pairs, so ds_read_b128 is conflict-free whether the LDS serves 8 or 16
+// lanes per cycle.
+constexpr int kPairBytes = (BM + BN) * 128;  // 64 KB
+FVSR_DEV int swz128(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
 
-// Stream K step kt (64 bytes of every row) into `slot`: wave w covers A rows
-// and B rows 64w .. 64w+63, four 1 KB (16-row) loads each; lane i of a load
-// lands at row 16*seg + i/4, physical chunk i%4.
-FVSR_DEV void issue_step(uint8_t LDS_AS* slot, const uint8_t* __restrict__ A, int64_t lda,
-                         const uint8_t* __restrict__ B, int64_t ldb, int64_t m0, int64_t n0,
-                         int64_t M, int64_t N, int64_t k0, int wave, int lane) {
-  const int p = lane & 3;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int seg = wave * 4 + t;
-    const int r = seg * 16 + (lane >> 2);
-    const int c = swz64(r, p);
-    int64_t ga = m0 + r, gb = n0 + r;
-    ga = ga < M ? ga : M - 1;
-    gb = gb < N ? gb : N - 1;
-    __builtin_amdgcn_global_load_lds(A + ga * lda + k0 + c * 16, (void LDS_AS*)(slot + seg * 1024),
-                                     16, 0, 0);
-    __builtin_amdgcn_global_load_lds(B + gb * ldb + k0 + c * 16,
-                                     (void LDS_AS*)(slot + BM * 64 + seg * 1024), 16, 0, 0);
-  }
-}
-
-// MFMA fragments of one K step: lane half h takes chunks 2h, 2h+1 of its row.
-FVSR_DEV void read_step(const uint8_t LDS_AS* slot, int wm, int wn, int lane, v8i (&fa)[4],
-                        v8i (&fb)[4]) {
-  const int h = lane >> 5;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = wm * 128 + j * 32 + (lane & 31);
-    const u32x4_t lo = *(const u32x4_t LDS_AS*)(slot + r * 64 + (swz64(r, 2 * h) << 4));
-    const u32x4_t hi = *(const u32x4_t LDS_AS*)(slot + r * 64 + (swz64(r, 2 * h + 1) << 4));
-    fa[j] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = wn * 128 + i * 32 + (lane & 31);
-    const uint8_t LDS_AS* b = slot + BM * 64;
-    const u32x4_t lo = *(const u32x4_t LDS_AS*)(b + r * 64 + (swz64(r, 2 * h) << 4));
-    const u32x4_t hi = *(const u32x4_t LDS_AS*)(b + r * 64 + (swz64(r, 2 * h + 1) << 4));
-    fb[i] = v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-  }
-}
-
-struct LoopCtx {
-  const uint8_t* A;
-  const uint8_t* B;
-  int64_t lda, ldb, m0, n0, M, N;
-  int KT, wave, wm, wn, lane;
+// Per-lane byte offsets of the 16-byte pieces this lane streams for one pair:
+// load t (of 8) of each operand covers rows 64*wave + 8*t .. +7, lane l taking
+// row 8*t + l/8 (clamped to the matrix) and the chunk that lands at position
+// l % 8.  Offsets fit 32 bits (checked on the host), so each load is a
+// uniform base plus a per-lane 32-bit offset.
+struct DmaOffs {
+  uint32_t a[8], b[8];
 };
 
-// s_waitcnt immediates (gfx9 encoding): vmcnt(n) with lgkmcnt/expcnt left open.
-constexpr int kWaitVm16 = 0x4F70;  // vmcnt(16): two K steps of this wave's loads in flight
-constexpr int kWaitVm8 = 0x0F78;   // vmcnt(8): one K step in flight
-constexpr int kWaitVm0 = 0x0F70;   // vmcnt(0)
-
-// Iteration kt: fragments of step kt are in (fa, fb).  Wait until step kt+1
-// has landed (every wave), start the loads of step kt+3 into `dma_slot` (the
-// slot of step kt-1, whose fragments every wave read before this barrier),
-// read step kt+1's fragments from `rd_slot` into (na, nb), then run step kt's
-// MFMAs.
-FVSR_DEV void k_iter(int kt, const LoopCtx& c, uint8_t LDS_AS* rd_slot, uint8_t LDS_AS* dma_slot,
-                     v16f (&acc)[4][4], v8i (&fa)[4], v8i (&fb)[4], v8i (&na)[4], v8i (&nb)[4]) {
-  if (kt >= c.KT) return;
-  if (kt + 1 < c.KT) {
-    if (kt + 2 < c.KT)
-      __builtin_amdgcn_s_waitcnt(kWaitVm8);
-    else
-      __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");  // no LDS access may move across the barrier
+FVSR_DEV void dma_offsets(DmaOffs& o, int64_t m0, int64_t n0, int64_t M, int64_t N, int64_t lda,
+                          int64_t ldb, int wave, int lane) {
+  const int rl = lane >> 3;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int r = wave * 64 + t * 8 + rl;
+    const int c = swz128(r, lane & 7);  // the swizzle is an involution in c
+    const int64_t ga = m0 + r < M ? m0 + r : M - 1;
+    const int64_t gb = n0 + r < N ? n0 + r : N - 1;
+    o.a[t] = (uint32_t)(ga * lda + c * 16);
+    o.b[t] = (uint32_t)(gb * ldb + c * 16);
   }
-  if (kt + 3 < c.KT)
-    issue_step(dma_slot, c.A, c.lda, c.B, c.ldb, c.m0, c.n0, c.M, c.N, (int64_t)(kt + 3) * 64,
-               c.wave, c.lane);
-  if (kt + 1 < c.KT) read_step(rd_slot, c.wm, c.wn, c.lane, na, nb);
-  mfma_block(acc, fa, fb);
 }
 
+// Raw buffer descriptor over `base` (stride 0, no range limit below 4 GB).
+FVSR_DEV i32x4_t make_rsrc(const void* base) {
+  const uint64_t p = (uint64_t)base;
+  return i32x4_t{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), -1, 0x00020000};
+}
+
+// Stream one pair (A and B bytes [k0, k0+128) of the tile's rows) into a pair
+// slot.  The per-lane offsets stay in VGPRs and k0 rides in the scalar offset.
+FVSR_DEV void issue_pair(uint8_t LDS_AS* slot, i32x4_t ra, i32x4_t rb, int k0, const DmaOffs& o,
+                         int wave) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int seg = wave * 8 + t;
+    fvsr_buffer_load_lds(ra, (void LDS_AS*)(slot + seg * 1024), 16, (int)o.a[t], k0, 0, 0);
+    fvsr_buffer_load_lds(rb, (void LDS_AS*)(slot + BM * 128 + seg * 1024), 16, (int)o.b[t], k0,
+                         0, 0);
+  }
+}
+
+// MFMA fragment of one 64-byte step (half `hs` of a pair) of row r: lane
+// half h takes logical chunks 4hs + 2h and 4hs + 2h + 1.
+FVSR_DEV v8i read_frag(const uint8_t LDS_AS* base, int r, int c0) {
+  const u32x4_t lo = *(const u32x4_t LDS_AS*)(base + r * 128 + (swz128(r, c0) << 4));
+  const u32x4_t hi = *(const u32x4_t LDS_AS*)(base + r * 128 + (swz128(r, c0 + 1) << 4));
+  return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+             (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+// All fragments of one step (A quadrant rows, then B quadrant rows).
+FVSR_DEV void read_step(const uint8_t LDS_AS* slot, int hs, int wm, int wn, int lane,
+                        v8i (&fa)[4], v8i (&fb)[4]) {
+  const int c0 = 4 * hs + 2 * (lane >> 5);
+  const int ra = wm * 128 + (lane & 31), rb = wn * 128 + (lane & 31);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fa[j] = read_frag(slot, ra + 32 * j, c0);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fb[i] = read_frag(slot + BM * 128, rb + 32 * i, c0);
+}
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSgMfma = 0x008, kSgVmemRead = 0x020, kSgDsRead = 0x100;
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4 (left open), lgkmcnt 11:8 (15 = left open).
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+constexpr int kWaitVm0 = waitcnt_imm(0, 15);
+
+struct RingCtx {
+  i32x4_t ra, rb;
+  int wave, wm, wn, lane;
+};
+
+// One 64-byte K step s of a tile (fragments of s in fa/fb):
+//   PAIR (s odd): wait until this wave's loads of the next pair (steps s+1,
+//     s+2) have landed and its reads of step s are done, then barrier: the
+//     pair is in LDS for every wave and the pair slot holding steps s-1, s
+//     is free; stream the pair of steps s+3, s+4 into it (`ds`, K offset k0,
+//     per-lane offsets `o`: the next tile's when past the end) -- two steps
+//     ahead of the reads that need it;
+//   read step s+1's fragments (pair slot `rd`, half RH) into na/nb;
+//   run the 16 MFMAs of step s (ZERO: start the accumulators from 0).
+// Loads and reads go out with the first eight MFMAs, leaving the second half
+// of the step for them to land.
+template <bool PAIR, int RH, bool ZERO>
+FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_t LDS_AS* rd,
+                        uint8_t LDS_AS* ds, v16f (&acc)[4][4], const v8i (&fa)[4],
+                        const v8i (&fb)[4], v8i (&na)[4], v8i (&nb)[4]) {
+  __builtin_amdgcn_sched_barrier(0);  // nothing (MFMAs included) moves across a step boundary
+  if (PAIR) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");  // no LDS access may move across the barrier
+    __builtin_amdgcn_sched_barrier(0);
+    issue_pair(ds, c.ra, c.rb, k0, o, c.wave);
+  }
+  read_step(rd, RH, c.wm, c.wn, c.lane, na, nb);
+  if (ZERO) {
+    const v16f z = {};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i], fa[j], z, 0, 0, 0, 0,
+                                                                     0, 0);
+  } else {
+    mfma_block(acc, fa, fb);
+  }
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    if (PAIR && q < 8) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+    if (q < 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
+  }
+}
+
+// Per-wave epilogue staging: 64 rows x 64 columns of bf16 (8 KB), one
+// quarter of the wave's 128 x 128 quadrant per pass; 8-byte units
+// XOR-swizzled with the row so that 16 lanes writing 16 rows cover all banks.
+FVSR_DEV int epi_off(int row, int unit) { return row * 128 + ((unit ^ (row & 15)) << 3); }
+
+// Scales and bias for column blocks i = 2 ip, 2 ip + 1: this lane's 4
+// consecutive columns for each (i, g).
+struct PassParams {
+  float sb[2][4][4];
+  uint32_t bias[2][4][2];
+};
+
+FVSR_DEV void load_pass_params(PassParams& pp, const EpiArgs& e, int64_t n0, int64_t N, int wn,
+                               int lane, int ip) {
+  const int h = lane >> 5;
+  const bool vec = e.vec_params && n0 + BN <= N;
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int64_t n = n0 + wn * 128 + (2 * ip + ii) * 32 + g * 8 + h * 4;
+      if (vec) {
+        const f32x4_t s = e.sb_col ? *(const f32x4_t*)(e.sb + n)
+                                   : f32x4_t{e.sb[0], e.sb[0], e.sb[0], e.sb[0]};
+        const u32x2_t b = e.bias ? *(const u32x2_t*)(e.bias + n) : u32x2_t{0u, 0u};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pp.sb[ii][g][r] = s[r];
+        pp.bias[ii][g][0] = b[0];
+        pp.bias[ii][g][1] = b[1];
+      } else {
+        uint32_t bb[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t ng = n + r < N ? n + r : N - 1;
+          pp.sb[ii][g][r] = e.sb[e.sb_col ? ng : 0];
+          bb[r] = e.bias ? (uint32_t)e.bias[ng] : 0u;
+        }
+        pp.bias[ii][g][0] = bb[0] | (bb[1] << 16);
+        pp.bias[ii][g][1] = bb[2] | (bb[3] << 16);
+      }
+    }
+}
+
+FVSR_DEV void load_row_scales(float (&sam)[4], const EpiArgs& e, int64_t m0, int64_t M, int wm,
+                              int lane) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t mg = m0 + wm * 128 + j * 32 + (lane & 31);
+    sam[j] = e.sa[e.sa_row ? (mg < M ? mg : M - 1) : 0];
+  }
+}
+
+// Phase 1 of pass (ip, jp): y = acc * (sa * sb) + bias for column blocks
+// 2ip, 2ip+1 and row blocks 2jp, 2jp+1, as bf16 into the staging area.
+FVSR_DEV void epi_stage(const v16f (&acc)[4][4], uint16_t LDS_AS* ep, int lane, int ip, int jp,
+                        const float (&sam)[4], const PassParams& pp) {
+  const int h = lane >> 5;
+#pragma unroll
+  for (int jj = 0; jj < 2; ++jj) {
+    const int j = 2 * jp + jj;
+    const int row = jj * 32 + (lane & 31);
+#pragma unroll
+    for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float y[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t bw = pp.bias[ii][g][r >> 1];
+          const float b = (r & 1) ? bf_hi(bw) : bf_lo(bw);
+          y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam[j] * pp.sb[ii][g][r]) + b;
+        }
+        *(u32x2_t LDS_AS*)((uint8_t LDS_AS*)ep + epi_off(row, ii * 8 + g * 2 + h)) =
+            u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+      }
+  }
+}
+
+// Phase 2 of pass (ip, jp): 64 rows of 64 columns leave as 16-byte chunks (8
+// lanes per row), with the gate-add / row-max epilogues applied on the way.
+template <int EPI>
+FVSR_DEV void epi_store(const uint16_t LDS_AS* ep, int64_t mw, int64_t nw, int64_t M, int64_t N,
+                        const EpiArgs& e, int lane, int ip, int jp, float (&vmax)[8]) {
+  const int c8 = lane & 7;
+  const int64_t n = nw + ip * 64 + c8 * 8;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int row = s * 8 + (lane >> 3);
+    const int64_t m = mw + jp * 64 + row;
+    const u32x2_t lo = *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)ep + epi_off(row, 2 * c8));
+    const u32x2_t hi =
+        *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)ep + epi_off(row, 2 * c8 + 1));
+    u32x4_t v = {lo[0], lo[1], hi[0], hi[1]};
+    if (EPI == FVSR_EPI_ROWMAX) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        if (n + 2 * w < N) vmax[s] = fmaxf(vmax[s], bf_lo(v[w]));
+        if (n + 2 * w + 1 < N) vmax[s] = fmaxf(vmax[s], bf_hi(v[w]));
+      }
+    }
+    if (m < M && n < N) {
+      uint16_t* cp = e.c + m * e.ldc + n;
+      if (EPI == FVSR_EPI_GATE_ADD) {
+        const uint16_t* rp = e.res + m * e.ldc + n;
+        if (n + 7 < N && ((((uintptr_t)cp) | (uintptr_t)rp | (uintptr_t)(e.gate + n)) & 15) == 0) {
+          const u32x4_t rv = *(const u32x4_t*)rp;
+          const u32x4_t gv = *(const u32x4_t*)(e.gate + n);
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const float t0 = round_bf16(bf_lo(gv[w]) * bf_lo(v[w]));
+            const float t1 = round_bf16(bf_hi(gv[w]) * bf_hi(v[w]));
+            v[w] = pack_bf16x2(bf_lo(rv[w]) + t0, bf_hi(rv[w]) + t1);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            if (n + q >= N) break;
+            const float y = (q & 1) ? bf_hi(v[q >> 1]) : bf_lo(v[q >> 1]);
+            const float t = round_bf16(bf2f(e.gate[n + q]) * y);
+            const float o = round_bf16(bf2f(rp[q]) + t);
+            const uint32_t ob = pack_bf16x2(o, 0.0f) & 0xffffu;
+            v[q >> 1] = (q & 1) ? ((v[q >> 1] & 0xffffu) | (ob << 16))
+                                : ((v[q >> 1] & 0xffff0000u) | ob);
+          }
+        }
+      }
+      if (n + 7 < N && (((uintptr_t)cp) & 15) == 0) {
+        *(u32x4_t*)cp = v;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (n + q < N) cp[q] = (uint16_t)((q & 1) ? (v[q >> 1] >> 16) : (v[q >> 1] & 0xffffu));
+      }
+    }
+  }
+}
+
+// Lane id recomputed where it is used: the epilogue's address arithmetic is
+// loop invariant, and computing it once outside the tile loop would keep a
+// few dozen VGPRs live across the whole main loop.
+FVSR_DEV int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t& n0) {
+  int tm, tn;
+  map_tile(t, tiles_m, tiles_n, tm, tn);
+  m0 = (int64_t)tm * BM;
+  n0 = (int64_t)tn * BN;
+}
+
+// Persistent kernel (K a multiple of 256, at least 512).  Workgroup b takes
+// tiles b, b + G, b + 2G, ... (G = grid size, a multiple of 8, so its tiles
+// stay within its XCD's M-grouped range).  The K steps of consecutive tiles
+// form one stream through the two pair slots: the last two pair loads of a
+// tile already fetch the next tile's pairs 0 and 1 (pair q lives in slot
+// q % 2, and K/128 is even) and its last step reads the next tile's step-0
+// fragments, so the epilogue overlaps the next tile's first loads.  The
+// epilogue stages through a spare 32 KB that no load targets (8 KB per
+// wave).  After a workgroup's last tile the same stream re-fetches that
+// tile's first pairs (harmless) and the workgroup drains its loads before it
+// exits.
 template <int EPI>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
                    int64_t ldb, int64_t M, int64_t N, int64_t K, EpiArgs ep) {
-  __shared__ __attribute__((aligned(1024))) uint8_t slot0[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot1[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot2[kSlotBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t slot3[kSlotBytes];
-  uint8_t LDS_AS* s0 = (uint8_t LDS_AS*)slot0;
-  uint8_t LDS_AS* s1 = (uint8_t LDS_AS*)slot1;
-  uint8_t LDS_AS* s2 = (uint8_t LDS_AS*)slot2;
-  uint8_t LDS_AS* s3 = (uint8_t LDS_AS*)slot3;
+  __shared__ __attribute__((aligned(1024))) uint8_t pair0[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t pair1[kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t spare[kSlotBytes];
+  uint8_t LDS_AS* p0 = (uint8_t LDS_AS*)pair0;
+  uint8_t LDS_AS* p1 = (uint8_t LDS_AS*)pair1;
 
   const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
-  int tm, tn;
-  map_tile(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  const int tiles = tiles_m * tiles_n;
+  int t = blockIdx.x;
+  if (t >= tiles) return;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  LoopCtx c{A, B, lda, ldb, (int64_t)tm * BM, (int64_t)tn * BN, M, N, (int)(K / 64), wave,
-            wave & 1, wave >> 1, lane};
+  const int wm = wave & 1, wn = wave >> 1;
+  uint16_t LDS_AS* epw = (uint16_t LDS_AS*)((uint8_t LDS_AS*)spare + wave * 8192);
+  const int KT = (int)(K / 64);
 
-  v16f acc[4][4];
-  zero_acc(acc);
-  v8i fa[4], fb[4], na[4], nb[4];
-  // Prologue: steps 0..2 in flight, wait for step 0, read its fragments.
-  issue_step(s0, A, lda, B, ldb, c.m0, c.n0, M, N, 0, wave, lane);
-  if (c.KT > 1) issue_step(s1, A, lda, B, ldb, c.m0, c.n0, M, N, 64, wave, lane);
-  if (c.KT > 2) issue_step(s2, A, lda, B, ldb, c.m0, c.n0, M, N, 128, wave, lane);
-  if (c.KT > 2)
-    __builtin_amdgcn_s_waitcnt(kWaitVm16);
-  else if (c.KT > 1)
-    __builtin_amdgcn_s_waitcnt(kWaitVm8);
-  else
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+  RingCtx c{make_rsrc(A), make_rsrc(B), wave, wm, wn, lane};
+  int64_t m0, n0;
+  tile_origin(t, tiles_m, tiles_n, m0, n0);
+  DmaOffs cur;
+  dma_offsets(cur, m0, n0, M, N, lda, ldb, wave, lane);
+  issue_pair(p0, c.ra, c.rb, 0, cur, wave);
+  issue_pair(p1, c.ra, c.rb, 128, cur, wave);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 15));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  read_step(s0, c.wm, c.wn, lane, fa, fb);
-  for (int kt = 0; kt < c.KT; kt += 4) {
-    k_iter(kt + 0, c, s1, s3, acc, fa, fb, na, nb);
-    k_iter(kt + 1, c, s2, s0, acc, na, nb, fa, fb);
-    k_iter(kt + 2, c, s3, s1, acc, fa, fb, na, nb);
-    k_iter(kt + 3, c, s0, s2, acc, na, nb, fa, fb);
+  v16f acc[4][4];
+  v8i fa[4], fb[4], na[4], nb[4];
+  read_step(p0, 0, wm, wn, lane, fa, fb);
+
+  for (;;) {
+    // First trip: steps 0-3 (accumulators start from 0 at step 0).
+    ring_step<false, 1, true>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<true, 0, false>(c, cur, 2 * 128, p1, p0, acc, na, nb, fa, fb);
+    ring_step<false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<true, 0, false>(c, cur, 3 * 128, p0, p1, acc, na, nb, fa, fb);
+    // Steady state: steps kt .. kt+3 load pairs kt/2 + 2 and kt/2 + 3.
+    for (int kt = 4; kt < KT - 4; kt += 4) {
+      ring_step<false, 1, false>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+      ring_step<true, 0, false>(c, cur, (kt + 4) * 64, p1, p0, acc, na, nb, fa, fb);
+      ring_step<false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+      ring_step<true, 0, false>(c, cur, (kt + 6) * 64, p0, p1, acc, na, nb, fa, fb);
+    }
+    // Last trip: steps KT-4 .. KT-1; their loads are the next tile's pairs 0
+    // and 1 and the last reads are the next tile's step 0.
+    const int tn = t + (int)gridDim.x;
+    int64_t m1 = m0, n1 = n0;
+    if (tn < tiles) tile_origin(tn, tiles_m, tiles_n, m1, n1);
+    DmaOffs nxt;
+    dma_offsets(nxt, m1, n1, M, N, lda, ldb, wave, lane);
+    ring_step<false, 1, false>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<true, 0, false>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
+    ring_step<false, 1, false>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<true, 0, false>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
+
+    // Epilogue (fa/fb now hold the next tile's step-0 fragments).
+    {
+      const int el = lane_here();
+      const int64_t mw = m0 + wm * 128, nw = n0 + wn * 128;
+      float sam[4];
+      load_row_scales(sam, ep, m0, M, wm, el);
+      float vmax[2][8];
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int s = 0; s < 8; ++s) vmax[q][s] = -__builtin_huge_valf();
+#pragma unroll
+      for (int ip = 0; ip < 2; ++ip) {
+        PassParams pp;
+        load_pass_params(pp, ep, n0, N, wn, el, ip);
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp) {
+          epi_stage(acc, epw, el, ip, jp, sam, pp);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          epi_store<EPI>(epw, mw, nw, M, N, ep, el, ip, jp, vmax[jp]);
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        }
+      }
+      if (EPI == FVSR_EPI_ROWMAX) {
+        // 8 lanes per row cover 64 columns per pass; both ip passes = the slab.
+#pragma unroll
+        for (int jp = 0; jp < 2; ++jp)
+#pragma unroll
+          for (int s = 0; s < 8; ++s) {
+            float v = vmax[jp][s];
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+            const int64_t m = mw + jp * 64 + s * 8 + (el >> 3);
+            if ((el & 7) == 0 && m < M && nw < N) ep.amax_part[m * ep.nparts + nw / 128] = v;
+          }
+      }
+    }
+    // Stores and the next tile's loads drain before the ring moves on.
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    t = tn;
+    if (t >= tiles) break;
+    m0 = m1;
+    n0 = n1;
+    cur = nxt;
   }
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  const CTile ct{{(uint16_t LDS_AS*)s0, (uint16_t LDS_AS*)s1, (uint16_t LDS_AS*)s2,
-                  (uint16_t LDS_AS*)s3}};
-  epilogue<EPI>(acc, ct, c.m0, c.n0, M, N, ep, c.wm, c.wn, lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -338,7 +614,7 @@ constexpr int BKG = 128;
 constexpr int kStageG = (BM + BN) * BKG;  // 64 KB
 constexpr int kChunksG = (BM * BKG / 16) / kThreads;  // 8
 
-FVSR_DEV int swz128(int row, int chunk) { return row * BKG + ((chunk ^ (row & 7)) << 4); }
+FVSR_DEV int swz_g(int row, int chunk) { return row * BKG + ((chunk ^ (row & 7)) << 4); }
 
 FVSR_DEV void load_stage_g(const uint8_t* __restrict__ g, int64_t ld, int64_t row0, int64_t rows,
                            int64_t k0, int64_t K, u32x4_t (&r)[kChunksG]) {
@@ -357,15 +633,15 @@ FVSR_DEV void store_stage_g(uint8_t LDS_AS* lds, const u32x4_t (&r)[kChunksG]) {
 #pragma unroll
   for (int i = 0; i < kChunksG; ++i) {
     const int id = threadIdx.x + kThreads * i;
-    *(u32x4_t LDS_AS*)(lds + swz128(id >> 3, id & 7)) = r[i];
+    *(u32x4_t LDS_AS*)(lds + swz_g(id >> 3, id & 7)) = r[i];
   }
 }
 
 FVSR_DEV v8i read_frag_g(const uint8_t LDS_AS* lds, int rb, int s, int lane) {
   const int row = rb + (lane & 31);
   const int c0 = s * 4 + (lane >> 5) * 2;
-  const u32x4_t lo = *(const u32x4_t LDS_AS*)(lds + swz128(row, c0));
-  const u32x4_t hi = *(const u32x4_t LDS_AS*)(lds + swz128(row, c0 + 1));
+  const u32x4_t lo = *(const u32x4_t LDS_AS*)(lds + swz_g(row, c0));
+  const u32x4_t hi = *(const u32x4_t LDS_AS*)(lds + swz_g(row, c0 + 1));
   return v8i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
              (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
@@ -421,14 +697,26 @@ void gemm_fp8_generic(const uint8_t* __restrict__ A, int64_t lda, const uint8_t*
 }
 
 template <int EPI>
-void launch(bool ring, unsigned tiles, hipStream_t st, const uint8_t* a, int64_t lda,
+void launch(bool ring, unsigned grid, hipStream_t st, const uint8_t* a, int64_t lda,
             const uint8_t* b, int64_t ldb, int64_t M, int64_t N, int64_t K, const EpiArgs& ep) {
   if (ring)
-    hipLaunchKernelGGL(gemm_fp8_ring<EPI>, dim3(tiles), dim3(kThreads), 0, st, a, lda, b, ldb, M,
-                       N, K, ep);
+    hipLaunchKernelGGL(gemm_fp8_ring<EPI>, dim3(grid), dim3(kThreads), 0, st, a, lda, b, ldb, M, N,
+                       K, ep);
   else
-    hipLaunchKernelGGL(gemm_fp8_generic<EPI>, dim3(tiles), dim3(kThreads), 0, st, a, lda, b, ldb,
+    hipLaunchKernelGGL(gemm_fp8_generic<EPI>, dim3(grid), dim3(kThreads), 0, st, a, lda, b, ldb,
                        M, N, K, ep);
+}
+
+// Workgroups of the persistent kernel: one per CU, rounded down to a multiple
+// of the 8 XCDs.
+unsigned persistent_grid(int64_t tiles) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 8)
+    cus = 256;
+  const int64_t g = (cus / 8) * 8;
+  return (unsigned)(tiles < g ? tiles : g);
 }
 
 }  // namespace
@@ -451,21 +739,27 @@ extern "C" int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa
   if (epilogue == FVSR_EPI_GATE_ADD && (!res || !gate)) return FVSR_EINVAL;
   const int64_t tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   if (tiles > 0x7fffffff) return FVSR_EUNSUPPORTED;
+  const int sb_col = sb_mode == FVSR_SCALE_ROW;
+  const int vec_params = (!sb_col || ((uintptr_t)sb & 15) == 0) && ((uintptr_t)bias & 7) == 0;
   EpiArgs ep{sa, sb, (const uint16_t*)bias, (uint16_t*)c, ldc, amax_part,
              fvsr_gemm_amax_parts(N), (const uint16_t*)res, (const uint16_t*)gate,
-             sa_mode == FVSR_SCALE_ROW, sb_mode == FVSR_SCALE_ROW};
+             sa_mode == FVSR_SCALE_ROW, sb_col, vec_params};
   hipStream_t st = (hipStream_t)stream;
-  const bool ring = K % 64 == 0 && K > 0;
+  // Persistent ring: K a multiple of 256, at least 8 K steps, and every row
+  // offset of either operand within 32 bits.
+  const bool ring = K % 256 == 0 && K >= 512 && K < 0x7fffffffLL && (M - 1) * lda + K <= 0xffffffffLL &&
+                    (N - 1) * ldb + K <= 0xffffffffLL;
+  const unsigned grid = ring ? persistent_grid(tiles) : (unsigned)tiles;
   const uint8_t *ap = (const uint8_t*)a, *bp = (const uint8_t*)b;
   switch (epilogue) {
     case FVSR_EPI_BIAS:
-      launch<FVSR_EPI_BIAS>(ring, (unsigned)tiles, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_BIAS>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
     case FVSR_EPI_ROWMAX:
-      launch<FVSR_EPI_ROWMAX>(ring, (unsigned)tiles, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_ROWMAX>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
     default:
-      launch<FVSR_EPI_GATE_ADD>(ring, (unsigned)tiles, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_GATE_ADD>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
   }
   return fvsr_launch_status();

@@ -195,7 +195,8 @@ def test_fp8_gemm_tensor_scales_and_golden(ops):
     _close_bf16(host_f(y), O.fp8_gemm(a2, sa, b2, sb))
 
 
-@pytest.mark.parametrize("MNK", [(1024, 8960, 1536), (300, 520, 256), (130, 200, 176)])
+@pytest.mark.parametrize("MNK", [(1024, 8960, 1536), (300, 520, 256), (130, 200, 176),
+                                 (4200, 4600, 512)])
 def test_gemm_rowmax_epilogue_and_gelu_requant(ops, MNK):
     """ROWMAX epilogue: same C as BIAS plus exact per-slab row maxima; the FFN
     requantisation (per token and per tensor) is bit-exact with
@@ -244,10 +245,12 @@ def test_gelu_tensor_quant_small_values(ops):
 
 
 @pytest.mark.parametrize("MNK", [(256, 256, 64), (300, 520, 192), (4224, 1536, 1536),
-                                 (1000, 600, 8960), (64, 64, 320)])
+                                 (1000, 600, 8960), (64, 64, 320), (4400, 4700, 512),
+                                 (2100, 9000, 768), (600, 300, 1280)])
 def test_fp8_gemm_ring_shapes(ops, MNK):
-    """The direct-to-LDS ring main loop (K a multiple of 64) across K-step
-    counts that exercise the unroll-by-four tail and ragged M, N."""
+    """The main-loop variants across K-step counts (persistent ring for K a
+    multiple of 256 and >= 512, register-staged loop otherwise), ragged M, N,
+    and more tiles than workgroups (several tiles per workgroup)."""
     M, N, K = MNK
     a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=M * 3 + K)
     y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(sa).to(DEV), codes_dev(b),
@@ -255,9 +258,10 @@ def test_fp8_gemm_ring_shapes(ops, MNK):
     _close_bf16(host_f(y), O.fp8_gemm(a, sa, b, sb, O.from_bf16_bits(bias)))
 
 
-def test_gemm_gate_add_epilogue(ops):
+@pytest.mark.parametrize("MNK", [(600, 1536, 512), (4200, 4600, 1024), (333, 1000, 8960)])
+def test_gemm_gate_add_epilogue(ops, MNK):
     from flashvsr_sm89_ops import _lib
-    M, N, K = 600, 1536, 512
+    M, N, K = MNK
     a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=3)
     ad, bd = codes_dev(a), codes_dev(b)
     sad, sbd = torch.from_numpy(sa).to(DEV), torch.from_numpy(sb).to(DEV)
