@@ -4,7 +4,9 @@
 
 Each csrc/*.hip is compiled to an object under _build/ in parallel, then
 linked into flashvsr_sm89_ops/libfvsr.so next to the Python package that
-loads it.  Flags: -O3 for gfx950 only, packed-fp32 instructions disabled
+loads it.  First, csrc/gelu_table_gen.c is compiled with gcc and run to
+write _build/gelu_table.inc (the bf16 GELU lookup table the quantisation
+kernels embed).  Flags: -O3 for gfx950 only, packed-fp32 instructions disabled
 (hipcc's host pass prints that it does not know the feature; harmless).
 """
 import argparse
@@ -22,8 +24,10 @@ LIB = os.path.join(HERE, "flashvsr_sm89_ops", "libfvsr.so")
 ARCH = os.environ.get("FVSR_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 
+CC = os.environ.get("CC", shutil.which("gcc") or "gcc")
+
 CFLAGS = [
-    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-I", OUT_DIR,
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function",
 ]
@@ -42,8 +46,23 @@ def _compile(src: str) -> str:
     return obj
 
 
+def _gelu_table() -> None:
+    """Generate _build/gelu_table.inc with the host generator."""
+    exe = os.path.join(OUT_DIR, "gelu_table_gen")
+    subprocess.run([CC, "-O2", "-std=c11", "-ffp-contract=off", "-fno-fast-math",
+                    os.path.join(CSRC, "gelu_table_gen.c"), "-o", exe, "-lm"], check=True)
+    out = subprocess.run([exe], check=True, capture_output=True, text=True).stdout
+    if out.count("0x") != 65536:
+        raise RuntimeError("gelu_table_gen produced a short table")
+    tmp = os.path.join(OUT_DIR, "gelu_table.inc.tmp")
+    with open(tmp, "w") as fh:
+        fh.write(out)
+    os.replace(tmp, os.path.join(OUT_DIR, "gelu_table.inc"))
+
+
 def build(jobs: int = 8) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
+    _gelu_table()
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(_compile, srcs))

@@ -42,62 +42,65 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
   const int64_t nchunk = D >> 3;
   const uint16_t* xr = x + row * D;
   float v[VPL][8];
+  u32x4_t raw[VPL], sraw[VPL], shraw[VPL];
+  const int64_t pb = (row / L) * D;
+  // All loads unconditional (past-the-end chunks read the last chunk again)
+  // so they are in flight together; repeated chunks are masked out of the
+  // sums below and change no maximum.
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
+    raw[j] = *(const u32x4_t*)(xr + cc * 8);
+    sraw[j] = *(const u32x4_t*)(scale + pb + cc * 8);
+    shraw[j] = *(const u32x4_t*)(shift + pb + cc * 8);
+  }
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
-      unpack8(*(const u32x4_t*)(xr + c * 8), v[j]);
+    const bool in = lane + 64 * j < nchunk;
+    unpack8(raw[j], v[j]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sum += v[j][e];
-    }
+    for (int e = 0; e < 8; ++e) sum += in ? v[j][e] : 0.0f;
   }
   const float mean = wave_sum(sum) / (float)D;
   float sq = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
+    const bool in = lane + 64 * j < nchunk;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        v[j][e] -= mean;
-        sq += v[j][e] * v[j][e];
-      }
+    for (int e = 0; e < 8; ++e) {
+      v[j][e] -= mean;
+      sq += in ? v[j][e] * v[j][e] : 0.0f;
     }
   }
   const float var = wave_sum(sq) / (float)D;
   const float den = sqrtf(var + eps);
-  const int64_t pb = (row / L) * D;
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
-      float s[8], sh[8];
-      unpack8(*(const u32x4_t*)(scale + pb + c * 8), s);
-      unpack8(*(const u32x4_t*)(shift + pb + c * 8), sh);
+    float s[8], sh[8];
+    unpack8(sraw[j], s);
+    unpack8(shraw[j], sh);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float xn = round_bf16(v[j][e] / den);
-        const float y = round_bf16(xn * round_bf16(1.0f + s[e]));
-        v[j][e] = round_bf16(y + sh[e]);
-        amax = fmaxf(amax, fabsf(v[j][e]));
-      }
-      if (WRITE_OUT) *(u32x4_t*)(out + row * D + c * 8) = pack8(v[j]);
+    for (int e = 0; e < 8; ++e) {
+      const float xn = round_bf16(v[j][e] / den);
+      const float y = round_bf16(xn * round_bf16(1.0f + s[e]));
+      v[j][e] = round_bf16(y + sh[e]);
+      amax = fmaxf(amax, fabsf(v[j][e]));
     }
+    if (WRITE_OUT && c < nchunk) *(u32x4_t*)(out + row * D + c * 8) = pack8(v[j]);
   }
   if (QUANT) {
     amax = wave_max(amax);
-    const float qs = fmaxf(amax, 1e-12f) / 448.0f;
+    const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
       const int64_t c = lane + 64 * j;
       if (c < nchunk) {
         u32x2_t q;
-        q[0] = pack_e4m3x4(clamp448(v[j][0] / qs), clamp448(v[j][1] / qs),
-                           clamp448(v[j][2] / qs), clamp448(v[j][3] / qs));
-        q[1] = pack_e4m3x4(clamp448(v[j][4] / qs), clamp448(v[j][5] / qs),
-                           clamp448(v[j][6] / qs), clamp448(v[j][7] / qs));
+        q[0] = e4m3x4_div(v[j][0], v[j][1], v[j][2], v[j][3], qs, qr);
+        q[1] = e4m3x4_div(v[j][4], v[j][5], v[j][6], v[j][7], qs, qr);
         *(u32x2_t*)(codes + row * D + c * 8) = q;
       }
     }
@@ -158,13 +161,10 @@ __global__ __launch_bounds__(kThreads) void gate_add_vec(
     u32x4_t xv[kGateUnroll], rv[kGateUnroll], gv[kGateUnroll];
 #pragma unroll
     for (int u = 0; u < kGateUnroll; ++u) {
-      const int64_t c = c0 + u * stride;
-      if (c < nchunk) {
-        const int64_t i = c * 8;
-        xv[u] = *(const u32x4_t*)(x + i);
-        rv[u] = *(const u32x4_t*)(res + i);
-        gv[u] = *(const u32x4_t*)(gate + (i / LD) * D + (i % D));
-      }
+      const int64_t i = clamp_chunk(c0 + u * stride, nchunk) * 8;
+      xv[u] = *(const u32x4_t*)(x + i);
+      rv[u] = *(const u32x4_t*)(res + i);
+      gv[u] = *(const u32x4_t*)(gate + (i / LD) * D + (i % D));
     }
 #pragma unroll
     for (int u = 0; u < kGateUnroll; ++u) {

@@ -40,6 +40,20 @@ FVSR_DEV uint32_t pack_e4m3x4(float a, float b, float c, float d) {
 
 FVSR_DEV float clamp448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 
+// Lane id, recomputed where it is used.  Address arithmetic derived from it
+// cannot be hoisted out of a loop by the compiler, which otherwise keeps a
+// loop-invariant offset per load alive (and spills them) for the whole loop.
+FVSR_DEV int lane_here() {
+  int l;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+  return l;
+}
+
+// Chunk index for an unconditional row load: chunks past the end of the row
+// read the row's last chunk (n >= 1) instead, so a wave issues all of its
+// row loads back to back rather than one per divergent branch.
+FVSR_DEV int64_t clamp_chunk(int64_t c, int64_t n) { return c < n ? c : n - 1; }
+
 // Wavefront (64-lane) reductions.
 FVSR_DEV float wave_max(float v) {
 #pragma unroll
@@ -88,6 +102,28 @@ FVSR_DEV float gelu_tanh_bf16(float x) {
   const float e = fvsr_expf(C2 * inner);
   const float t = 1.0f - 2.0f / (e + 1.0f);
   return round_bf16((0.5f * x) * (1.0f + t));
+}
+
+// e4m3 codes of clamp(v_i / s, +-448) for four values, where v_i / s is the
+// IEEE fp32 division the quantisation contract prescribes.  With r = 1/s
+// (IEEE), y = fl(v * r) lies within 1.5 * 2^-23 (relative) of fl(v / s), so
+// fl(v / s) lies between y * (1 - 2^-21) and y * (1 + 2^-21) (each rounded).
+// When the e4m3 roundings (monotone) of both ends agree, that is the code;
+// otherwise a rounding boundary lies inside the bracket and the division
+// itself decides (rare; taken per wave only when some lane needs it).
+FVSR_DEV uint32_t e4m3x4_div(float v0, float v1, float v2, float v3, float s, float r) {
+  const float kLo = 0.99999952316284180f, kHi = 1.00000047683715820f;  // 1 -+ 2^-21
+  const float y0 = v0 * r, y1 = v1 * r, y2 = v2 * r, y3 = v3 * r;
+  const uint32_t lo = pack_e4m3x4(clamp448(y0 * kLo), clamp448(y1 * kLo), clamp448(y2 * kLo),
+                                  clamp448(y3 * kLo));
+  const uint32_t hi = pack_e4m3x4(clamp448(y0 * kHi), clamp448(y1 * kHi), clamp448(y2 * kHi),
+                                  clamp448(y3 * kHi));
+  uint32_t out = lo;
+  if (__builtin_amdgcn_ballot_w64(lo != hi)) {
+    if (lo != hi)
+      out = pack_e4m3x4(clamp448(v0 / s), clamp448(v1 / s), clamp448(v2 / s), clamp448(v3 / s));
+  }
+  return out;
 }
 
 // Largest |GELU| over negative inputs is 0.16992 (exhaustive over bf16), and

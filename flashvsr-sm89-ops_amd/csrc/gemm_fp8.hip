@@ -474,15 +474,6 @@ FVSR_DEV void epi_store(const uint16_t LDS_AS* ep, int64_t mw, int64_t nw, int64
   }
 }
 
-// Lane id recomputed where it is used: the epilogue's address arithmetic is
-// loop invariant, and computing it once outside the tile loop would keep a
-// few dozen VGPRs live across the whole main loop.
-FVSR_DEV int lane_here() {
-  int l;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
-  return l;
-}
-
 FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t& n0) {
   int tm, tn;
   map_tile(t, tiles_m, tiles_n, tm, tn);

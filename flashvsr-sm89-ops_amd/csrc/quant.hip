@@ -7,8 +7,14 @@
 // re-reduces those partials (at most 1024 floats) before quantising, so no
 // atomics and no memset are needed.
 //
-// Bit-exactness: x/s is an IEEE division (never x * (1/s)); the fp32 ->
-// e4m3fn conversion is v_cvt_pk_fp8_f32 after clamping to +-448.
+// Bit-exactness: the codes are those of the IEEE division x/s (e4m3x4_div
+// multiplies by 1/s and falls back to the division whenever the product's
+// bracket straddles an e4m3 rounding boundary); the fp32 -> e4m3fn
+// conversion is v_cvt_pk_fp8_f32 after clamping to +-448.
+//
+// GELU of bf16 data (the FFN requantisation) is a lookup: the 65536 bf16
+// results, generated at build time from the operation sequence of
+// gelu_tanh_bf16 (csrc/gelu_table_gen.c), sit in every workgroup's LDS.
 #pragma clang fp contract(off)
 #include "common.h"
 
@@ -41,13 +47,12 @@ FVSR_DEV float chunk_absmax(u32x4_t c) {
   return m;
 }
 
-FVSR_DEV u32x2_t chunk_codes(u32x4_t c, float s) {
-  u32x2_t r;
-  r[0] = pack_e4m3x4(clamp448(bf_lo(c[0]) / s), clamp448(bf_hi(c[0]) / s),
-                     clamp448(bf_lo(c[1]) / s), clamp448(bf_hi(c[1]) / s));
-  r[1] = pack_e4m3x4(clamp448(bf_lo(c[2]) / s), clamp448(bf_hi(c[2]) / s),
-                     clamp448(bf_lo(c[3]) / s), clamp448(bf_hi(c[3]) / s));
-  return r;
+// Codes of 8 bf16 values (x/s each); r = 1/s.
+FVSR_DEV u32x2_t chunk_codes(u32x4_t c, float s, float r) {
+  u32x2_t q;
+  q[0] = e4m3x4_div(bf_lo(c[0]), bf_hi(c[0]), bf_lo(c[1]), bf_hi(c[1]), s, r);
+  q[1] = e4m3x4_div(bf_lo(c[2]), bf_hi(c[2]), bf_lo(c[3]), bf_hi(c[3]), s, r);
+  return q;
 }
 
 FVSR_DEV float qscale(float amax) { return fmaxf(amax, 1e-12f) / 448.0f; }
@@ -65,25 +70,108 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec(
   const uint16_t* xr = x + row * ld;
   const int64_t nchunk = cols >> 3;
   u32x4_t v[VPL];
+  // Every lane loads VPL chunks, past-the-end ones clamped to the row's last
+  // chunk: the loads stay unconditional (so they are all in flight at once)
+  // and a repeated chunk cannot change the row's max.
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) v[j] = *(const u32x4_t*)(xr + clamp_chunk(lane + 64 * j, nchunk) * 8);
   float m = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
-      v[j] = *(const u32x4_t*)(xr + c * 8);
-      if (GELU) v[j] = gelu_chunk(v[j]);
-      m = fmaxf(m, chunk_absmax(v[j]));
-    }
+    if (GELU) v[j] = gelu_chunk(v[j]);
+    m = fmaxf(m, chunk_absmax(v[j]));
   }
   const float amax = wave_max(m);
-  const float s = qscale(amax);
+  const float s = qscale(amax), r = 1.0f / s;
   uint8_t* qr = codes + row * cols;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t c = lane + 64 * j;
-    if (c < nchunk) *(u32x2_t*)(qr + c * 8) = chunk_codes(v[j], s);
+    if (c < nchunk) *(u32x2_t*)(qr + c * 8) = chunk_codes(v[j], s, r);
   }
   if (lane == 0) scale_out[row] = amax / 448.0f;
+}
+
+// ---------------------------------------------------------------------------
+// Row mode with GELU by table: persistent workgroups of 8 waves (one per CU,
+// the 128 KB table fills most of its LDS), one row per wave at a time, row in
+// registers (cols % 8 == 0, cols <= 512*VPL, 16-byte rows), the wave's next
+// row loading while it works on the current one.
+// ---------------------------------------------------------------------------
+__device__ const uint16_t kGeluTable[65536] __attribute__((aligned(16))) = {
+#include "gelu_table.inc"
+};
+
+constexpr int kTabWaves = 8;
+
+FVSR_DEV u32x4_t gelu_lookup(u32x4_t c, const uint16_t* tab) {
+  u32x4_t g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    g[i] = (uint32_t)tab[c[i] & 0xffffu] | ((uint32_t)tab[c[i] >> 16] << 16);
+  return g;
+}
+
+// Load row `row` (chunks past the end of the row repeat its last chunk).
+template <int VPL>
+FVSR_DEV void load_row(u32x4_t (&v)[VPL], const uint16_t* x, int64_t row, int64_t ld, int nchunk) {
+  const int lane = lane_here();
+  const uint8_t* xr = (const uint8_t*)(x + row * ld);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j < nchunk ? lane + 64 * j : nchunk - 1;
+    v[j] = *(const u32x4_t*)(xr + (uint32_t)c * 16u);
+  }
+}
+
+template <int VPL>
+FVSR_DEV void gelu_quant_row(u32x4_t (&v)[VPL], const uint16_t* tab, int64_t row, int64_t cols,
+                             int nchunk, uint8_t* codes, float* scale_out) {
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    v[j] = gelu_lookup(v[j], tab);
+    m = fmaxf(m, chunk_absmax(v[j]));  // a repeated chunk changes no maximum
+  }
+  const float amax = wave_max(m);
+  const float s = qscale(amax), r = 1.0f / s;
+  const int lane = lane_here();
+  uint8_t* qr = codes + row * cols;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nchunk) *(u32x2_t*)(qr + (uint32_t)c * 8u) = chunk_codes(v[j], s, r);
+  }
+  if (lane == 0) scale_out[row] = amax / 448.0f;
+}
+
+template <int VPL>
+__global__ __launch_bounds__(kTabWaves * 64) void quant_rows_gelu_table(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+  for (int i = threadIdx.x; i < 65536 / 8; i += kTabWaves * 64)
+    ((u32x4_t*)tab)[i] = ((const u32x4_t*)kGeluTable)[i];
+  __syncthreads();
+  const int nchunk = (int)(cols >> 3);
+  const int64_t stride = (int64_t)gridDim.x * kTabWaves;
+  int64_t row = (int64_t)blockIdx.x * kTabWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  u32x4_t va[VPL], vb[VPL];
+  load_row(va, x, row, ld, nchunk);
+  for (;;) {
+    int64_t next = row + stride;
+    load_row(vb, x, next < rows ? next : rows - 1, ld, nchunk);
+    gelu_quant_row(va, tab, row, cols, nchunk, codes, scale_out);
+    if (next >= rows) break;
+    row = next;
+    next = row + stride;
+    load_row(va, x, next < rows ? next : rows - 1, ld, nchunk);
+    gelu_quant_row(vb, tab, row, cols, nchunk, codes, scale_out);
+    if (next >= rows) break;
+    row = next;
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the last prefetch (a repeated row) drains before exit
 }
 
 // Row mode, any shape: two passes over the row (the second hits L2).
@@ -173,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
     float* __restrict__ scale_out) {
   __shared__ float red[kWaves];
   const float amax = reduce_partials(part, nparts, red);
-  const float s = qscale(amax);
+  const float s = qscale(amax), r = 1.0f / s;
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = amax / 448.0f;
   const int lane = threadIdx.x & 63;
   for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
@@ -184,7 +272,7 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
       for (int64_t c = lane; c < (cols >> 3); c += 64) {
         u32x4_t v = *(const u32x4_t*)(xr + c * 8);
         if (GELU) v = gelu_chunk(v);
-        *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s);
+        *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s, r);
       }
     } else {
       for (int64_t c = lane; c < cols; c += 64) {
@@ -276,13 +364,28 @@ int partial_blocks(int64_t rows) {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// Compute units of the current device (persistent grids).
+int64_t cu_count() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < 1)
+    cus = 256;
+  return cus;
+}
+
 template <bool GELU>
 int launch_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8_t* q,
                 float* s, hipStream_t st) {
   const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
   const bool vec = (cols % 8 == 0) && (ld % 8 == 0) && aligned16(x) && aligned16(q);
   const int64_t vpl = (cols / 8 + 63) / 64;
-  if (vec && vpl <= 3) {
+  if (GELU && vec && vpl <= 18) {
+    const int64_t want = (rows + kTabWaves - 1) / kTabWaves;
+    const int64_t g = want < cu_count() ? want : cu_count();
+    hipLaunchKernelGGL((quant_rows_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0, st,
+                       x, rows, cols, ld, q, s);
+  } else if (vec && vpl <= 3) {
     hipLaunchKernelGGL((quant_rows_vec<3, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
   } else if (vec && vpl <= 6) {
     hipLaunchKernelGGL((quant_rows_vec<6, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);

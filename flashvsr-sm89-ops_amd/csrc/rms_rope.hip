@@ -19,46 +19,52 @@ FVSR_DEV void rms_rope_row(const uint16_t* xr, const uint16_t* __restrict__ w,
                            int64_t D, int64_t head_dim, float eps, int lane) {
   const int64_t nchunk = D >> 3;
   u32x4_t v[VPL];
+  // Unconditional loads (past-the-end chunks read the last chunk again, and
+  // are masked out of the sum) so that the row's loads are in flight together.
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) v[j] = *(const u32x4_t*)(xr + clamp_chunk(lane + 64 * j, nchunk) * 8);
   float sq = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
-      v[j] = *(const u32x4_t*)(xr + c * 8);
+    const bool in = lane + 64 * j < nchunk;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = bf_lo(v[j][i]), b = bf_hi(v[j][i]);
-        sq += a * a + b * b;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float a = bf_lo(v[j][i]), b = bf_hi(v[j][i]);
+      sq += in ? a * a + b * b : 0.0f;
+    }
+  }
+  // Weights and (cos, sin) for every chunk, loaded before the reduction
+  // completes (same clamping).
+  u32x4_t wv[VPL];
+  f32x4_t cs0[VPL], cs1[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
+    wv[j] = *(const u32x4_t*)(w + cc * 8);
+    if (ROPE) {
+      const int64_t i0 = ((cc * 8) % head_dim) >> 1;  // first pair index of this chunk
+      cs0[j] = *(const f32x4_t*)(cs_row + 2 * i0);     // c0 s0 c1 s1
+      cs1[j] = *(const f32x4_t*)(cs_row + 2 * i0 + 4); // c2 s2 c3 s3
     }
   }
   const float r = rsqrtf(wave_sum(sq) / (float)D + eps);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t c = lane + 64 * j;
-    if (c < nchunk) {
-      const u32x4_t wv = *(const u32x4_t*)(w + c * 8);
-      u32x4_t o;
-      f32x4_t cs0, cs1;
-      if (ROPE) {
-        const int64_t i0 = ((c * 8) % head_dim) >> 1;  // first pair index of this chunk
-        cs0 = *(const f32x4_t*)(cs_row + 2 * i0);       // c0 s0 c1 s1
-        cs1 = *(const f32x4_t*)(cs_row + 2 * i0 + 4);   // c2 s2 c3 s3
-      }
+    u32x4_t o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ye = round_bf16(bf_lo(v[j][i]) * r) * bf_lo(wv[i]);
-        const float yo = round_bf16(bf_hi(v[j][i]) * r) * bf_hi(wv[i]);
-        if (ROPE) {
-          const float cc = i < 2 ? cs0[2 * i] : cs1[2 * (i - 2)];
-          const float ss = i < 2 ? cs0[2 * i + 1] : cs1[2 * (i - 2) + 1];
-          o[i] = pack_bf16x2(ye * cc - yo * ss, ye * ss + yo * cc);
-        } else {
-          o[i] = pack_bf16x2(ye, yo);
-        }
+    for (int i = 0; i < 4; ++i) {
+      const float ye = round_bf16(bf_lo(v[j][i]) * r) * bf_lo(wv[j][i]);
+      const float yo = round_bf16(bf_hi(v[j][i]) * r) * bf_hi(wv[j][i]);
+      if (ROPE) {
+        const float cc = i < 2 ? cs0[j][2 * i] : cs1[j][2 * (i - 2)];
+        const float ss = i < 2 ? cs0[j][2 * i + 1] : cs1[j][2 * (i - 2) + 1];
+        o[i] = pack_bf16x2(ye * cc - yo * ss, ye * ss + yo * cc);
+      } else {
+        o[i] = pack_bf16x2(ye, yo);
       }
-      *(u32x4_t*)(outr + c * 8) = o;
     }
+    if (c < nchunk) *(u32x4_t*)(outr + c * 8) = o;
   }
 }
 

@@ -106,6 +106,61 @@ def test_e4m3_conversion_all_bf16_patterns(ops):
     assert np.array_equal(host_codes(q).reshape(-1), O.e4m3_encode(O.from_bf16_bits(vals)))
 
 
+def _rows_of(vals, cols, head):
+    """Split `vals` into rows of `cols` bf16 patterns, each row starting with
+    the patterns in `head` (pins the row's amax); zero padded."""
+    body = cols - len(head)
+    n = -(-len(vals) // body)
+    out = np.zeros((n, cols), np.uint16)
+    out[:, :len(head)] = head
+    flat = np.zeros(n * body, np.uint16)
+    flat[:len(vals)] = vals
+    out[:, len(head):] = flat.reshape(n, body)
+    return out
+
+
+def test_e4m3_fast_division_register_rows(ops):
+    """The register-resident row kernels multiply by 1/s and fall back to the
+    IEEE division near e4m3 rounding boundaries.  (a) Every finite bf16 value
+    with |v| <= 448, rows pinned at amax 448 (s = 1: every e4m3 midpoint that
+    bf16 can hold is hit exactly).  (b) e4m3 midpoints scaled by an inexact
+    s = 3/448 and their bf16 neighbours, so x*(1/s) and x/s can straddle."""
+    b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = O.from_bf16_bits(b)
+    keep = np.isfinite(f) & (np.abs(f) <= 448)
+    x = _rows_of(b[keep], 8960, np.uint16([O.bf16_bits(np.float32([448.0]))[0]]))
+    q, s = ops.quantize_fp8(dev_bf16(x), per_token=True)
+    rq, rs = O.quantize_fp8(x, per_row=True)
+    assert np.array_equal(host_codes(q), rq) and np.array_equal(host_f(s).reshape(-1), rs)
+    codes = np.arange(256, dtype=np.uint8)
+    ev = O.e4m3_decode(codes)
+    ev = np.sort(ev[np.isfinite(ev)])
+    mids = (ev[1:] + ev[:-1]) / 2
+    sc = np.float32(3.0) / np.float32(448.0)
+    centre = O.bf16_bits((mids * sc).astype(np.float32)).astype(np.int32)
+    near = np.concatenate([centre + d for d in (-2, -1, 0, 1, 2)]).astype(np.uint16)
+    near = near[np.isfinite(O.from_bf16_bits(near)) & (np.abs(O.from_bf16_bits(near)) < 3.0)]
+    x = _rows_of(near, 1536, np.uint16([O.bf16_bits(np.float32([3.0]))[0]]))
+    q, s = ops.quantize_fp8(dev_bf16(x), per_token=True)
+    rq, rs = O.quantize_fp8(x, per_row=True)
+    assert np.array_equal(host_codes(q), rq) and np.array_equal(host_f(s).reshape(-1), rs)
+
+
+def test_gelu_quant_all_bf16_by_table(ops):
+    """Per-token GELU requantisation (table lookup in LDS) over every finite
+    bf16 pattern, rows grouped by magnitude so each row's scale keeps the
+    codes informative: codes and scales bit-exact with the oracle's GELU."""
+    b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    f = O.from_bf16_bits(b)
+    fin = b[np.isfinite(f)]
+    order = np.argsort(np.abs(O.from_bf16_bits(fin)), kind="stable")
+    x = _rows_of(fin[order], 8960, np.zeros(0, np.uint16))
+    q, s = ops.fused_gelu_quant_fp8(dev_bf16(x), per_token=True)
+    rq, rs = O.quantize_fp8(x, per_row=True, gelu=True)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+    assert np.array_equal(host_codes(q), rq)
+
+
 @pytest.mark.parametrize("shape", [(64, 8960), (5, 1003), (16, 1024)])
 @pytest.mark.parametrize("per_token", [True, False])
 def test_gelu_quant_bitexact(ops, shape, per_token):
