@@ -195,7 +195,13 @@ void bsa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   __shared__ __attribute__((aligned(1024))) uint8_t stage1[kStage];
   uint8_t LDS_AS* st0 = (uint8_t LDS_AS*)stage0;
   uint8_t LDS_AS* st1 = (uint8_t LDS_AS*)stage1;
-  const int h = blockIdx.x / NQ, qb = blockIdx.x % NQ;
+  // Workgroup ids are dispatched round robin over the 8 XCDs; give each XCD a
+  // contiguous range of (head, query block) units so that neighbouring query
+  // blocks, whose local windows share most key blocks, share one L2.
+  const int total = (int)gridDim.x, per = total / 8, rem = total % 8;
+  const int xcd = blockIdx.x % 8, loc = blockIdx.x / 8;
+  const int unit = xcd < rem ? xcd * (per + 1) + loc : rem * (per + 1) + (xcd - rem) * per + loc;
+  const int h = unit / NQ, qb = unit % NQ;
   const int lane = threadIdx.x & 63, half = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = cnt[(int64_t)h * NQ + qb];
