@@ -362,13 +362,14 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-# Kernel (name fragment, grid size in work-items) of each op of the C5 stack,
-# for finding its dispatches in a counter file.  gemm_o_gate and
-# gemm_ffn2_gate share kernel and grid, so neither can be told apart there.
+# Kernel (name fragment, grid size in work-items or None) of each op of the C5
+# stack whose dispatches can be told apart in a counter file.  The GEMMs run
+# persistent grids of one workgroup per CU, so their dispatches share a name
+# and a grid and are not listed.
 OP_KERNELS = {
     "bsa": ("bsa_fwd_kernel<true>", None),
-    "gemm_qkv": ("gemm_fp8_ring<0>", 66 * 18 * 256),
-    "gemm_ffn0": ("gemm_fp8_ring<0>", 66 * 35 * 256),
+    "gelu_quant": ("quant_rows_gelu_table", None),
+    "rms_rope_qk": ("rms_rope_qk_vec", None),
 }
 
 

@@ -15,6 +15,10 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+#ifndef FVSR_LN_ROWS
+#define FVSR_LN_ROWS 2
+#endif
+constexpr int kLnRows = FVSR_LN_ROWS;  // rows per wavefront in ln_modulate_vec
 
 FVSR_DEV void unpack8(u32x4_t c, float* f) {
 #pragma unroll
@@ -24,6 +28,15 @@ FVSR_DEV void unpack8(u32x4_t c, float* f) {
   }
 }
 
+// Packed bf16 pair whose halves are then read back separately: the empty asm
+// keeps the single two-value conversion (the compiler otherwise rewrites each
+// half's read-back into its own conversion).
+FVSR_DEV uint32_t pack_bf16x2_once(float a, float b) {
+  uint32_t w = pack_bf16x2(a, b);
+  asm("" : "+v"(w));
+  return w;
+}
+
 FVSR_DEV u32x4_t pack8(const float* f) {
   u32x4_t c;
 #pragma unroll
@@ -31,80 +44,166 @@ FVSR_DEV u32x4_t pack8(const float* f) {
   return c;
 }
 
-template <int VPL, bool WRITE_OUT, bool QUANT>
+// bf16(v_e / den) for the eight values of a chunk, as four packed bf16 pairs,
+// from the reciprocal rd = 1/den (IEEE).  For normal y = fl(v * rd), y lies
+// within 1.5 * 2^-23 (relative) of fl(v / den), so fl(v / den) lies between
+// fl(y * (1 - 2^-21)) and fl(y * (1 + 2^-21)); bf16 rounding is monotone, so
+// when both ends round to the same bf16 that is the result.  Lanes whose ends
+// disagree set `bad`.  The caller guarantees that no y is subnormal, infinite
+// or NaN (see ln_fast_ok).
+FVSR_DEV u32x4_t bf16_quot8(const float* v, float rd, bool& bad) {
+  const float kLo = 0.99999952316284180f, kHi = 1.00000047683715820f;  // 1 -+ 2^-21
+  u32x4_t out;
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    const float y0 = v[2 * p] * rd, y1 = v[2 * p + 1] * rd;
+    const uint32_t lo = pack_bf16x2_once(y0 * kLo, y1 * kLo);
+    const uint32_t hi = pack_bf16x2(y0 * kHi, y1 * kHi);
+    bad |= lo != hi;
+    out[p] = lo;
+  }
+  return out;
+}
+
+// Row-level precondition of bf16_quot8.  A nonzero v = fl(x - mean), x bf16
+// and mean fp32 normal, has |v| >= |mean| * 2^-24: within a factor of two of
+// mean (Sterbenz) both are multiples of mean's fp32 ulp, otherwise
+// |v| >= |mean| / 2.  So |mean| * rd >= 2^-100 keeps every nonzero
+// y = v * rd above 2^-125 (normal); y is bounded by sqrt(D) (a normalised
+// value).  NaN or infinite rows fail the test and take the division.
+FVSR_DEV bool ln_fast_ok(float mean, float rd) {
+  const float am = fabsf(mean);
+  return am >= 0x1p-125f && am * rd >= 0x1p-100f && rd <= 0x1p100f;
+}
+
+// R rows of one batch element per wavefront: the modulation vectors
+// bf16(1 + scale) and shift are loaded and prepared once for the R rows, and
+// all R rows are loaded before any arithmetic, so each wave keeps R row loads
+// in flight.  Row groups never straddle a batch element; a group running
+// past the batch's last row recomputes that row and stores nothing for it.
+template <int VPL, int R, bool WRITE_OUT, bool QUANT>
 __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
-    const uint16_t* __restrict__ shift, uint16_t* __restrict__ out, int64_t rows, int64_t L,
+    const uint16_t* __restrict__ shift, uint16_t* __restrict__ out, int64_t B, int64_t L,
     int64_t D, float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  const int64_t groups = (L + R - 1) / R;
+  const int64_t g = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (g >= B * groups) return;
+  const int64_t b = g / groups;
+  const int64_t l0 = (g - b * groups) * R;
   const int64_t nchunk = D >> 3;
-  const uint16_t* xr = x + row * D;
-  float v[VPL][8];
-  u32x4_t raw[VPL], sraw[VPL], shraw[VPL];
-  const int64_t pb = (row / L) * D;
+  const int64_t pb = b * D;
+  int64_t row[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) row[r] = b * L + (l0 + r < L ? l0 + r : L - 1);
   // All loads unconditional (past-the-end chunks read the last chunk again)
   // so they are in flight together; repeated chunks are masked out of the
   // sums below and change no maximum.
+  u32x4_t raw[R][VPL], sraw[VPL], shraw[VPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      raw[r][j] = *(const u32x4_t*)(x + row[r] * D + clamp_chunk(lane + 64 * j, nchunk) * 8);
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
-    raw[j] = *(const u32x4_t*)(xr + cc * 8);
     sraw[j] = *(const u32x4_t*)(scale + pb + cc * 8);
     shraw[j] = *(const u32x4_t*)(shift + pb + cc * 8);
   }
-  float sum = 0.0f;
+  float v[R][VPL][8], sum[R];
 #pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const bool in = lane + 64 * j < nchunk;
-    unpack8(raw[j], v[j]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sum += in ? v[j][e] : 0.0f;
-  }
-  const float mean = wave_sum(sum) / (float)D;
-  float sq = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const bool in = lane + 64 * j < nchunk;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[j][e] -= mean;
-      sq += in ? v[j][e] * v[j][e] : 0.0f;
-    }
-  }
-  const float var = wave_sum(sq) / (float)D;
-  const float den = sqrtf(var + eps);
-  float amax = 0.0f;
-#pragma unroll
-  for (int j = 0; j < VPL; ++j) {
-    const int64_t c = lane + 64 * j;
-    float s[8], sh[8];
-    unpack8(sraw[j], s);
-    unpack8(shraw[j], sh);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float xn = round_bf16(v[j][e] / den);
-      const float y = round_bf16(xn * round_bf16(1.0f + s[e]));
-      v[j][e] = round_bf16(y + sh[e]);
-      amax = fmaxf(amax, fabsf(v[j][e]));
-    }
-    if (WRITE_OUT && c < nchunk) *(u32x4_t*)(out + row * D + c * 8) = pack8(v[j]);
-  }
-  if (QUANT) {
-    amax = wave_max(amax);
-    const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
+  for (int r = 0; r < R; ++r) {
+    sum[r] = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
-      const int64_t c = lane + 64 * j;
-      if (c < nchunk) {
-        u32x2_t q;
-        q[0] = e4m3x4_div(v[j][0], v[j][1], v[j][2], v[j][3], qs, qr);
-        q[1] = e4m3x4_div(v[j][4], v[j][5], v[j][6], v[j][7], qs, qr);
-        *(u32x2_t*)(codes + row * D + c * 8) = q;
+      unpack8(raw[r][j], v[r][j]);
+      float cs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs += v[r][j][e];
+      sum[r] += lane + 64 * j < nchunk ? cs : 0.0f;
+    }
+  }
+  float sq[R], mean_r[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float mean = wave_sum(sum[r]) / (float)D;
+    sq[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float cs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[r][j][e] -= mean;
+        cs = __builtin_fmaf(v[r][j][e], v[r][j][e], cs);
+      }
+      sq[r] += lane + 64 * j < nchunk ? cs : 0.0f;
+    }
+    mean_r[r] = mean;
+  }
+  float s1[VPL][8], sh[VPL][8];  // bf16(1 + scale) and shift
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    unpack8(shraw[j], sh[j]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t w = pack_bf16x2_once(1.0f + bf_lo(sraw[j][p]), 1.0f + bf_hi(sraw[j][p]));
+      s1[j][2 * p] = bf_lo(w);
+      s1[j][2 * p + 1] = bf_hi(w);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float den = sqrtf(wave_sum(sq[r]) / (float)D + eps);
+    const float rd = 1.0f / den;
+    u32x4_t xn[VPL];
+    bool bad = !ln_fast_ok(mean_r[r], rd);
+    if (!bad) {
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) xn[j] = bf16_quot8(v[r][j], rd, bad);
+    }
+    if (__builtin_amdgcn_ballot_w64(bad)) {
+      if (bad) {
+#pragma unroll
+        for (int j = 0; j < VPL; ++j)
+#pragma unroll
+          for (int p = 0; p < 4; ++p)
+            xn[j][p] = pack_bf16x2_once(v[r][j][2 * p] / den, v[r][j][2 * p + 1] / den);
       }
     }
-    if (lane == 0) row_scale[row] = amax / 448.0f;
+    // y = bf16(xn * bf16(1 + s)); out = bf16(y + shift), two values per
+    // conversion.  The row's largest |out| is kept as two bf16 magnitudes
+    // (an unsigned 16-bit maximum orders non-negative bf16, NaN largest).
+    u32x4_t o[VPL];
+    u16x2_t mx = {0, 0};
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint32_t y = pack_bf16x2_once(bf_lo(xn[j][p]) * s1[j][2 * p],
+                                            bf_hi(xn[j][p]) * s1[j][2 * p + 1]);
+        o[j][p] = pack_bf16x2_once(bf_lo(y) + sh[j][2 * p], bf_hi(y) + sh[j][2 * p + 1]);
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, o[j][p] & 0x7fff7fffu));
+      }
+      const int64_t c = lane + 64 * j;
+      if (WRITE_OUT && c < nchunk && l0 + r < L) *(u32x4_t*)(out + row[r] * D + c * 8) = o[j];
+    }
+    if (QUANT) {
+      const float amax = wave_max_abs(fmaxf(bf2f(mx[0]), bf2f(mx[1])));
+      const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t c = lane + 64 * j;
+        if (c < nchunk && l0 + r < L) {
+          u32x2_t q;
+          q[0] = e4m3x4_div(bf_lo(o[j][0]), bf_hi(o[j][0]), bf_lo(o[j][1]), bf_hi(o[j][1]), qs, qr);
+          q[1] = e4m3x4_div(bf_lo(o[j][2]), bf_hi(o[j][2]), bf_lo(o[j][3]), bf_hi(o[j][3]), qs, qr);
+          *(u32x2_t*)(codes + row[r] * D + c * 8) = q;
+        }
+      }
+      if (lane == 0 && l0 + r < L) row_scale[row[r]] = amax / 448.0f;
+    }
   }
 }
 
@@ -214,15 +313,17 @@ extern "C" int fvsr_ln_modulate(const void* x, const void* scale, const void* sh
   const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(scale) &&
                    aligned16(shift) && (!out || aligned16(out)) && (!codes || aligned16(codes));
   if (vec) {
+    const int64_t groups = B * ((L + kLnRows - 1) / kLnRows);
+    const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves));
     if (out && codes)
-      hipLaunchKernelGGL((ln_modulate_vec<3, true, true>), grid, block, 0, st, xp, sp, hp, op,
-                         rows, L, D, eps, qp, row_scale);
+      hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, true, true>), vgrid, block, 0, st, xp, sp,
+                         hp, op, B, L, D, eps, qp, row_scale);
     else if (out)
-      hipLaunchKernelGGL((ln_modulate_vec<3, true, false>), grid, block, 0, st, xp, sp, hp, op,
-                         rows, L, D, eps, qp, row_scale);
+      hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, true, false>), vgrid, block, 0, st, xp, sp,
+                         hp, op, B, L, D, eps, qp, row_scale);
     else
-      hipLaunchKernelGGL((ln_modulate_vec<3, false, true>), grid, block, 0, st, xp, sp, hp, op,
-                         rows, L, D, eps, qp, row_scale);
+      hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, false, true>), vgrid, block, 0, st, xp, sp,
+                         hp, op, B, L, D, eps, qp, row_scale);
   } else {
     hipLaunchKernelGGL(ln_modulate_generic, grid, block, 0, st, xp, sp, hp, op, rows, L, D, eps,
                        qp, row_scale);

@@ -4,8 +4,10 @@
 // uint16_t, e4m3fn tensors are uint8_t.  Conversions use the gfx950
 // instructions whose rounding was checked against torch's casts:
 //   fp32 -> bf16   v_cvt_pk_bf16_f32 (round to nearest even)
-//   fp32 -> e4m3fn v_cvt_pk_fp8_f32  (round to nearest even; inputs are
-//                  always clamped to +-448 first, so overflow never occurs)
+//   fp32 -> e4m3fn v_cvt_pk_fp8_f32  (round to nearest even; magnitudes in
+//                  (448, 464] give 448, the tie at 464 included, and larger
+//                  ones NaN, so inputs are either clamped to +-448 first or
+//                  known to stay below 464)
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -18,6 +20,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint16_t u16x2_t __attribute__((ext_vector_type(2)));
 
 FVSR_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 FVSR_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -31,7 +34,7 @@ FVSR_DEV uint32_t pack_bf16x2(float a, float b) {
 // fp32 -> bf16 -> fp32 (the "round-trip through bf16" of eager).
 FVSR_DEV float round_bf16(float a) { return bf_lo(pack_bf16x2(a, 0.0f)); }
 
-// Four fp32 (already within +-448) -> four e4m3fn codes in one dword.
+// Four fp32 (of magnitude below 464) -> four e4m3fn codes in one dword.
 FVSR_DEV uint32_t pack_e4m3x4(float a, float b, float c, float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
@@ -54,16 +57,56 @@ FVSR_DEV int lane_here() {
 // row loads back to back rather than one per divergent branch.
 FVSR_DEV int64_t clamp_chunk(int64_t c, int64_t n) { return c < n ? c : n - 1; }
 
-// Wavefront (64-lane) reductions.
-FVSR_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+// Wavefront (64-lane) reductions on the VALU through DPP lane moves (no LDS
+// round trips): quad swaps, half-row and row mirrors leave every lane of a
+// 16-lane row with the row's result; two row broadcasts fold rows 0..3 into
+// lane 63, which is read into a scalar register, so the result is uniform.
+// Lanes of rows outside a broadcast's row mask receive 0 (the identity for
+// sums, and for maxima of non-negative values).
+template <int CTRL, int ROWS>
+FVSR_DEV float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false));
+}
+FVSR_DEV float lane63(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 FVSR_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f32<0xB1, 0xf>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E, 0xf>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141, 0xf>(v);  // row_half_mirror
+  v += dpp_f32<0x140, 0xf>(v);  // row_mirror
+  v += dpp_f32<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_f32<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+  return lane63(v);
+}
+// Maximum of non-negative values (|x| maxima): compared as unsigned bit
+// patterns, which orders non-negative floats and lets a NaN win.
+FVSR_DEV float umax_f32(float a, float b) {
+  const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
+  return __builtin_bit_cast(float, x > y ? x : y);
+}
+FVSR_DEV float wave_max_abs(float v) {
+  v = umax_f32(v, dpp_f32<0xB1, 0xf>(v));
+  v = umax_f32(v, dpp_f32<0x4E, 0xf>(v));
+  v = umax_f32(v, dpp_f32<0x141, 0xf>(v));
+  v = umax_f32(v, dpp_f32<0x140, 0xf>(v));
+  v = umax_f32(v, dpp_f32<0x142, 0xa>(v));
+  v = umax_f32(v, dpp_f32<0x143, 0xc>(v));
+  return lane63(v);
+}
+// Maximum of any values: the row broadcasts fill masked-out rows with 0, so
+// they are replaced by a final lane-63 read of each row's own maximum.
+FVSR_DEV float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xB1, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x4E, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x141, 0xf>(v));
+  v = fmaxf(v, dpp_f32<0x140, 0xf>(v));
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // Shared fp32 exp for y clamped to [-40, 40] (the GELU below is saturated
@@ -111,13 +154,14 @@ FVSR_DEV float gelu_tanh_bf16(float x) {
 // When the e4m3 roundings (monotone) of both ends agree, that is the code;
 // otherwise a rounding boundary lies inside the bracket and the division
 // itself decides (rare; taken per wave only when some lane needs it).
+// Precondition: |v_i| <= 448 * s, as for s = max(amax, 1e-12) / 448 over
+// values bounded by amax; then both ends stay below 449 and convert without
+// a clamp (conversions below 464 round to at most 448).
 FVSR_DEV uint32_t e4m3x4_div(float v0, float v1, float v2, float v3, float s, float r) {
   const float kLo = 0.99999952316284180f, kHi = 1.00000047683715820f;  // 1 -+ 2^-21
   const float y0 = v0 * r, y1 = v1 * r, y2 = v2 * r, y3 = v3 * r;
-  const uint32_t lo = pack_e4m3x4(clamp448(y0 * kLo), clamp448(y1 * kLo), clamp448(y2 * kLo),
-                                  clamp448(y3 * kLo));
-  const uint32_t hi = pack_e4m3x4(clamp448(y0 * kHi), clamp448(y1 * kHi), clamp448(y2 * kHi),
-                                  clamp448(y3 * kHi));
+  const uint32_t lo = pack_e4m3x4(y0 * kLo, y1 * kLo, y2 * kLo, y3 * kLo);
+  const uint32_t hi = pack_e4m3x4(y0 * kHi, y1 * kHi, y2 * kHi, y3 * kHi);
   uint32_t out = lo;
   if (__builtin_amdgcn_ballot_w64(lo != hi)) {
     if (lo != hi)

@@ -81,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec(
     if (GELU) v[j] = gelu_chunk(v[j]);
     m = fmaxf(m, chunk_absmax(v[j]));
   }
-  const float amax = wave_max(m);
+  const float amax = wave_max_abs(m);
   const float s = qscale(amax), r = 1.0f / s;
   uint8_t* qr = codes + row * cols;
 #pragma unroll
@@ -133,7 +133,7 @@ FVSR_DEV void gelu_quant_row(u32x4_t (&v)[VPL], const uint16_t* tab, int64_t row
     v[j] = gelu_lookup(v[j], tab);
     m = fmaxf(m, chunk_absmax(v[j]));  // a repeated chunk changes no maximum
   }
-  const float amax = wave_max(m);
+  const float amax = wave_max_abs(m);
   const float s = qscale(amax), r = 1.0f / s;
   const int lane = lane_here();
   uint8_t* qr = codes + row * cols;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic(
   const uint16_t* xr = x + row * ld;
   float m = 0.0f;
   for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(xr + c)));
-  const float amax = wave_max(m);
+  const float amax = wave_max_abs(m);
   const float s = qscale(amax);
   uint8_t* qr = codes + row * cols;
   for (int64_t c = lane; c < cols; c += 64) {
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic(
 // Tensor mode.
 // ---------------------------------------------------------------------------
 FVSR_DEV float block_max(float m, float* red) {
-  m = wave_max(m);
+  m = wave_max_abs(m);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
   float r = red[0];
@@ -337,7 +337,7 @@ __global__ __launch_bounds__(kThreads) void quant_weight_rows(
   const uint16_t* wr = w + row * k;
   float m = 0.0f;
   for (int64_t c = lane; c < k; c += 64) m = fmaxf(m, fabsf(bf2f(wr[c])));
-  const float s = weight_scale(wave_max(m));
+  const float s = weight_scale(wave_max_abs(m));
   for (int64_t c = lane; c < k; c += 64) codes[row * k + c] = weight_code(bf2f(wr[c]), s, true);
   if (lane == 0) scale_out[row] = s;
 }
