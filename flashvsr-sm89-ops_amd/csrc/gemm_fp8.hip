@@ -303,8 +303,9 @@ struct RingCtx {
 //     ahead of the reads that need it;
 //   read step s+1's fragments (pair slot `rd`, half RH) into na/nb;
 //   run the 16 MFMAs of step s (ZERO: start the accumulators from 0).
-// Loads and reads go out with the first eight MFMAs, leaving the second half
-// of the step for them to land.
+// The sixteen loads go out one per MFMA (a burst of them stalls the wave's
+// instruction stream) and the reads with the first eight MFMAs, leaving the
+// second half of the step for them to land.
 template <bool PAIR, int RH, bool ZERO>
 FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_t LDS_AS* rd,
                         uint8_t LDS_AS* ds, v16f (&acc)[4][4], const v8i (&fa)[4],
@@ -331,104 +332,94 @@ FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_
   }
 #pragma unroll
   for (int q = 0; q < 16; ++q) {
-    if (PAIR && q < 8) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 2, 0);
+    if (PAIR) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
     __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
     if (q < 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
   }
 }
 
-// Per-wave epilogue staging: 64 rows x 64 columns of bf16 (8 KB), one
-// quarter of the wave's 128 x 128 quadrant per pass; 8-byte units
-// XOR-swizzled with the row so that 16 lanes writing 16 rows cover all banks.
+// Per-wave epilogue area: 32 rows x 64 columns of bf16 staging (4 KB, one
+// eighth of the wave's 128 x 128 quadrant per pass; 8-byte units XOR-swizzled
+// with the row so that 16 lanes writing 16 rows cover all banks), then the
+// quadrant's epilogue parameters: sa of its 128 rows, sb and bias of its 128
+// columns (1.25 KB).
+constexpr int kEpiStageBytes = 32 * 128;
+constexpr int kEpiWaveBytes = kEpiStageBytes + 128 * 4 + 128 * 4 + 128 * 2;
 FVSR_DEV int epi_off(int row, int unit) { return row * 128 + ((unit ^ (row & 15)) << 3); }
 
-// Scales and bias for column blocks i = 2 ip, 2 ip + 1: this lane's 4
-// consecutive columns for each (i, g).
-struct PassParams {
-  float sb[2][4][4];
-  uint32_t bias[2][4][2];
+// This lane's share of the quadrant's parameters (rows / columns q*64 + lane),
+// loaded into registers ahead of time and parked in LDS by put_epi_params.
+struct EpiParamRegs {
+  float sa[2], sb[2];
+  uint32_t bias[2];
 };
 
-FVSR_DEV void load_pass_params(PassParams& pp, const EpiArgs& e, int64_t n0, int64_t N, int wn,
-                               int lane, int ip) {
+FVSR_DEV void fetch_epi_params(EpiParamRegs& r, const EpiArgs& e, int64_t m0, int64_t n0,
+                               int64_t M, int64_t N, int wm, int wn, int lane) {
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int64_t m = m0 + wm * 128 + q * 64 + lane, n = n0 + wn * 128 + q * 64 + lane;
+    const int64_t mc = m < M ? m : M - 1, nc = n < N ? n : N - 1;
+    r.sa[q] = e.sa[e.sa_row ? mc : 0];
+    r.sb[q] = e.sb[e.sb_col ? nc : 0];
+    r.bias[q] = e.bias ? (uint32_t)e.bias[nc] : 0u;
+  }
+}
+
+FVSR_DEV void put_epi_params(const EpiParamRegs& r, uint8_t LDS_AS* prm, int lane) {
+  float LDS_AS* sa_l = (float LDS_AS*)prm;
+  float LDS_AS* sb_l = sa_l + 128;
+  uint16_t LDS_AS* bi_l = (uint16_t LDS_AS*)(sb_l + 128);
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    sa_l[q * 64 + lane] = r.sa[q];
+    sb_l[q * 64 + lane] = r.sb[q];
+    bi_l[q * 64 + lane] = (uint16_t)r.bias[q];
+  }
+}
+
+// Phase 1 of pass (ip, j): y = acc * (sa * sb) + bias for column blocks
+// 2ip, 2ip+1 and row block j, as bf16 into the staging area.
+FVSR_DEV void epi_stage(const v16f (&acc)[4][4], uint16_t LDS_AS* stg,
+                        const uint8_t LDS_AS* prm, int lane, int ip, int j) {
+  const float LDS_AS* sa_l = (const float LDS_AS*)prm;
+  const float LDS_AS* sb_l = sa_l + 128;
+  const uint16_t LDS_AS* bi_l = (const uint16_t LDS_AS*)(sb_l + 128);
   const int h = lane >> 5;
-  const bool vec = e.vec_params && n0 + BN <= N;
+  const int row = lane & 31;
+  const float sam = sa_l[j * 32 + row];
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int64_t n = n0 + wn * 128 + (2 * ip + ii) * 32 + g * 8 + h * 4;
-      if (vec) {
-        const f32x4_t s = e.sb_col ? *(const f32x4_t*)(e.sb + n)
-                                   : f32x4_t{e.sb[0], e.sb[0], e.sb[0], e.sb[0]};
-        const u32x2_t b = e.bias ? *(const u32x2_t*)(e.bias + n) : u32x2_t{0u, 0u};
+      const int cl = (2 * ip + ii) * 32 + g * 8 + h * 4;
+      const f32x4_t sb = *(const f32x4_t LDS_AS*)(sb_l + cl);
+      const u32x2_t bw = *(const u32x2_t LDS_AS*)(bi_l + cl);
+      float y[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pp.sb[ii][g][r] = s[r];
-        pp.bias[ii][g][0] = b[0];
-        pp.bias[ii][g][1] = b[1];
-      } else {
-        uint32_t bb[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t ng = n + r < N ? n + r : N - 1;
-          pp.sb[ii][g][r] = e.sb[e.sb_col ? ng : 0];
-          bb[r] = e.bias ? (uint32_t)e.bias[ng] : 0u;
-        }
-        pp.bias[ii][g][0] = bb[0] | (bb[1] << 16);
-        pp.bias[ii][g][1] = bb[2] | (bb[3] << 16);
+      for (int r = 0; r < 4; ++r) {
+        const float b = (r & 1) ? bf_hi(bw[r >> 1]) : bf_lo(bw[r >> 1]);
+        y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam * sb[r]) + b;
       }
+      *(u32x2_t LDS_AS*)((uint8_t LDS_AS*)stg + epi_off(row, ii * 8 + g * 2 + h)) =
+          u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
     }
 }
 
-FVSR_DEV void load_row_scales(float (&sam)[4], const EpiArgs& e, int64_t m0, int64_t M, int wm,
-                              int lane) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t mg = m0 + wm * 128 + j * 32 + (lane & 31);
-    sam[j] = e.sa[e.sa_row ? (mg < M ? mg : M - 1) : 0];
-  }
-}
-
-// Phase 1 of pass (ip, jp): y = acc * (sa * sb) + bias for column blocks
-// 2ip, 2ip+1 and row blocks 2jp, 2jp+1, as bf16 into the staging area.
-FVSR_DEV void epi_stage(const v16f (&acc)[4][4], uint16_t LDS_AS* ep, int lane, int ip, int jp,
-                        const float (&sam)[4], const PassParams& pp) {
-  const int h = lane >> 5;
-#pragma unroll
-  for (int jj = 0; jj < 2; ++jj) {
-    const int j = 2 * jp + jj;
-    const int row = jj * 32 + (lane & 31);
-#pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        float y[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t bw = pp.bias[ii][g][r >> 1];
-          const float b = (r & 1) ? bf_hi(bw) : bf_lo(bw);
-          y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam[j] * pp.sb[ii][g][r]) + b;
-        }
-        *(u32x2_t LDS_AS*)((uint8_t LDS_AS*)ep + epi_off(row, ii * 8 + g * 2 + h)) =
-            u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
-      }
-  }
-}
-
-// Phase 2 of pass (ip, jp): 64 rows of 64 columns leave as 16-byte chunks (8
+// Phase 2 of pass (ip, j): 32 rows of 64 columns leave as 16-byte chunks (8
 // lanes per row), with the gate-add / row-max epilogues applied on the way.
 template <int EPI>
-FVSR_DEV void epi_store(const uint16_t LDS_AS* ep, int64_t mw, int64_t nw, int64_t M, int64_t N,
-                        const EpiArgs& e, int lane, int ip, int jp, float (&vmax)[8]) {
+FVSR_DEV void epi_store(const uint16_t LDS_AS* stg, int64_t mw, int64_t nw, int64_t M, int64_t N,
+                        const EpiArgs& e, int lane, int ip, int j, float (&vmax)[4]) {
   const int c8 = lane & 7;
   const int64_t n = nw + ip * 64 + c8 * 8;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
+  for (int s = 0; s < 4; ++s) {
     const int row = s * 8 + (lane >> 3);
-    const int64_t m = mw + jp * 64 + row;
-    const u32x2_t lo = *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)ep + epi_off(row, 2 * c8));
+    const int64_t m = mw + j * 32 + row;
+    const u32x2_t lo = *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)stg + epi_off(row, 2 * c8));
     const u32x2_t hi =
-        *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)ep + epi_off(row, 2 * c8 + 1));
+        *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)stg + epi_off(row, 2 * c8 + 1));
     u32x4_t v = {lo[0], lo[1], hi[0], hi[1]};
     if (EPI == FVSR_EPI_ROWMAX) {
 #pragma unroll
@@ -498,7 +489,7 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
                    int64_t ldb, int64_t M, int64_t N, int64_t K, EpiArgs ep) {
   __shared__ __attribute__((aligned(1024))) uint8_t pair0[kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t pair1[kPairBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t spare[kSlotBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t spare[4 * kEpiWaveBytes];
   uint8_t LDS_AS* p0 = (uint8_t LDS_AS*)pair0;
   uint8_t LDS_AS* p1 = (uint8_t LDS_AS*)pair1;
 
@@ -509,7 +500,9 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave & 1, wn = wave >> 1;
-  uint16_t LDS_AS* epw = (uint16_t LDS_AS*)((uint8_t LDS_AS*)spare + wave * 8192);
+  uint8_t LDS_AS* epa = (uint8_t LDS_AS*)spare + wave * kEpiWaveBytes;
+  uint16_t LDS_AS* stg = (uint16_t LDS_AS*)epa;
+  uint8_t LDS_AS* prm = epa + kEpiStageBytes;
   const int KT = (int)(K / 64);
 
   RingCtx c{make_rsrc(A), make_rsrc(B), wave, wm, wn, lane};
@@ -546,44 +539,42 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
     if (tn < tiles) tile_origin(tn, tiles_m, tiles_n, m1, n1);
     DmaOffs nxt;
     dma_offsets(nxt, m1, n1, M, N, lda, ldb, wave, lane);
+    // This tile's epilogue parameters load under the last trip's MFMAs.
+    EpiParamRegs epr;
+    fetch_epi_params(epr, ep, m0, n0, M, N, wm, wn, lane);
     ring_step<false, 1, false>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
     ring_step<true, 0, false>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
     ring_step<false, 1, false>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
     ring_step<true, 0, false>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
 
-    // Epilogue (fa/fb now hold the next tile's step-0 fragments).
+    // Epilogue (fa/fb now hold the next tile's step-0 fragments): eight
+    // passes of 32 rows x 64 columns through the wave's own staging area.
     {
       const int el = lane_here();
       const int64_t mw = m0 + wm * 128, nw = n0 + wn * 128;
-      float sam[4];
-      load_row_scales(sam, ep, m0, M, wm, el);
-      float vmax[2][8];
+      put_epi_params(epr, prm, el);
+      float vmax[4][4];
 #pragma unroll
-      for (int q = 0; q < 2; ++q)
+      for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int s = 0; s < 8; ++s) vmax[q][s] = -__builtin_huge_valf();
+        for (int s = 0; s < 4; ++s) vmax[j][s] = -__builtin_huge_valf();
 #pragma unroll
-      for (int ip = 0; ip < 2; ++ip) {
-        PassParams pp;
-        load_pass_params(pp, ep, n0, N, wn, el, ip);
+      for (int ip = 0; ip < 2; ++ip)
 #pragma unroll
-        for (int jp = 0; jp < 2; ++jp) {
-          epi_stage(acc, epw, el, ip, jp, sam, pp);
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          epi_store<EPI>(epw, mw, nw, M, N, ep, el, ip, jp, vmax[jp]);
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        for (int j = 0; j < 4; ++j) {
+          epi_stage(acc, stg, prm, el, ip, j);
+          epi_store<EPI>(stg, mw, nw, M, N, ep, el, ip, j, vmax[j]);
         }
-      }
       if (EPI == FVSR_EPI_ROWMAX) {
         // 8 lanes per row cover 64 columns per pass; both ip passes = the slab.
 #pragma unroll
-        for (int jp = 0; jp < 2; ++jp)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int s = 0; s < 8; ++s) {
-            float v = vmax[jp][s];
+          for (int s = 0; s < 4; ++s) {
+            float v = vmax[j][s];
 #pragma unroll
             for (int o = 4; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-            const int64_t m = mw + jp * 64 + s * 8 + (el >> 3);
+            const int64_t m = mw + j * 32 + s * 8 + (el >> 3);
             if ((el & 7) == 0 && m < M && nw < N) ep.amax_part[m * ep.nparts + nw / 128] = v;
           }
       }
