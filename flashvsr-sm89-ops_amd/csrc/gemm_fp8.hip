@@ -46,7 +46,6 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256;
 constexpr int kThreads = 256;
 constexpr int kGroupM = 8;
-constexpr int kSlotBytes = (BM + BN) * 64;  // 32 KB
 
 struct EpiArgs {
   const float* sa;

@@ -47,6 +47,9 @@ _SIGS = {
     "fvsr_rms_rope_qk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I64, _I64,
                           _P], _I),
     "fvsr_block_index": ([_P, _I64, _I64, _I64, _P, _P, _P], _I),
+    "fvsr_draft_workspace_floats": ([_I64, _I64, _I64, _I64], _I64),
+    "fvsr_draft_block_mask": ([_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P,
+                               _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P], _I),
     "fvsr_bsa_fwd": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64,
                       _I64, _I64, _I64, _F, _P, _P, _P], _I),
 }

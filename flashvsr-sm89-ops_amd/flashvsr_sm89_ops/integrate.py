@@ -13,7 +13,11 @@ and before ``pipe.init_cross_kv()``.  In dependency order it
    ``DiTBlock.forward`` with fused-aware copies whose stock branches are the
    upstream math, so each flag can be switched off (``FS89_FUSED_ROPE``,
    ``FS89_FUSED_ADALN``);
-4. resolves ``block_sparse_attn`` to the HIP block-sparse attention.
+4. resolves ``block_sparse_attn`` to the HIP block-sparse attention;
+   ``FS89_DRAFT=1`` also computes the draft block mask on the device
+   (``lcsa/draft.py``, the bf16 reading of lcsa/reference.py:37-64) in place
+   of the DiT's ``generate_draft_block_mask`` (default off: the DiT's own
+   function is the one the reference calls).
 
 Re-running ``enable`` on a patched pipeline is safe.  ``FS89_TCDEC_COMPILE``
 (torch.compile of the decoder MemBlocks) is accepted but not applied: it is a
@@ -108,7 +112,10 @@ def _make_self_attn_forward(dit):
             self.local_attn_mask_h = h // 8
             self.local_attn_mask_w = w // 8
             self.local_range = local_range
-        attention_mask = dit.generate_draft_block_mask(
+        draft = dit.generate_draft_block_mask
+        if _FLAG("FS89_DRAFT", "0"):
+            from .lcsa.draft import generate_draft_block_mask as draft
+        attention_mask = draft(
             B, self.num_heads, seqlen, q_w, k_w, topk=topk, local_attn_mask=self.local_attn_mask)
 
         x = self.attn(reorder_q, reorder_k, reorder_v, attention_mask)

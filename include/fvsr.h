@@ -160,6 +160,33 @@ int fvsr_rms_rope_qk(const void* q, const void* k, const void* wq, const void* w
 int fvsr_block_index(const uint8_t* keep, int64_t H, int64_t NQ, int64_t NK, int32_t* sel,
                      int32_t* cnt, void* stream);
 
+/* Number of 32-bit floats of workspace fvsr_draft_block_mask needs. */
+int64_t fvsr_draft_workspace_floats(int64_t H, int64_t D, int64_t NQ, int64_t NK);
+
+/*
+ * Draft block mask, reference draft_block_mask (flashvsr_sm89_ops/lcsa/
+ * reference.py:37-64), the work of the dit.generate_draft_block_mask call at
+ * integrate.py:103-104: window-mean pooling of q and k over each 128-token
+ * block, scores avg_q.avg_k / sqrt(D) per head, -inf outside the local rule
+ * local[l % sq][m % sk] (uint8 [sq, sk]), softmax over key blocks, and a joint
+ * top-k per (head, query time row) over the time row's NQ/q_temporal query
+ * blocks x NK key blocks: keep = attn > the (topk+1)-th largest attn.  Every
+ * stage is rounded to bf16 as torch does for bf16 q/k.
+ * q, k: bf16, token j of block n at row map[n*128 + j] (row n*128 + j when the
+ * map is NULL), rows q_tok_stride / k_tok_stride elements apart; H*D channels.
+ * Outputs (either or both): keep uint8 [H, NQ, NK]; sel int32 [H, NQ, NK] and
+ * cnt int32 [H, NQ] in fvsr_block_index's form (kept block ids ascending).
+ * workspace: fvsr_draft_workspace_floats(H, D, NQ, NK).
+ * Requires D % 8 == 0, token strides % 8 == 0, 16-byte aligned q and k, and
+ * D + NK <= 12288.
+ */
+int fvsr_draft_block_mask(const void* q, int64_t q_tok_stride, const int32_t* q_map,
+                          const void* k, int64_t k_tok_stride, const int32_t* k_map, int64_t H,
+                          int64_t D, int64_t NQ, int64_t NK, int64_t q_temporal,
+                          const uint8_t* local, int64_t sq, int64_t sk, int64_t topk,
+                          uint8_t* keep, int32_t* sel, int32_t* cnt, float* workspace,
+                          int64_t workspace_floats, void* stream);
+
 /*
  * Block-sparse attention over 128-token blocks, reference _bsa_fwd_kernel /
  * block_sparse_attention (lcsa/triton_lcsa.py:19-61,74-94): for each head h

@@ -272,29 +272,71 @@ def build_local_block_mask(bh: int, bw: int, rng: int) -> np.ndarray:
     return in_row & in_col
 
 
-def draft_block_mask(q_w, k_w, nheads: int, q_temporal: int, local: np.ndarray, topk: int):
+def _topk_threshold_keep(flat: np.ndarray, topk: int) -> np.ndarray:
+    """keep = flat > the (k+1)-th largest value of each row, k = min(topk,
+    n-1), in torch.topk's order (NaN above every number; lcsa/reference.py:59-62)."""
+    k = min(flat.shape[1] - 1, topk)
+    order = np.where(np.isnan(flat), np.inf, flat)  # attn <= 1: inf only stands for NaN
+    thr = -np.sort(-order, axis=1)[:, k]
+    thr = np.where(np.isinf(thr), np.nan, thr)[:, None]
+    with np.errstate(invalid="ignore"):
+        return flat > thr
+
+
+def draft_block_mask(q_w, k_w, nheads: int, q_temporal: int, local: np.ndarray, topk: int,
+                     return_attn: bool = False):
     """Window-mean pooled block scores -> local mask -> softmax -> joint top-k
-    per (head, query time row) (lcsa/reference.py:37-64).  Returns [h,Nq,Nk] bool."""
-    avg_q = np.asarray(q_w, np.float32).mean(1)
-    avg_k = np.asarray(k_w, np.float32).mean(1)
-    Nq, HD = avg_q.shape
-    Nk = avg_k.shape[0]
-    D = HD // nheads
-    aq = avg_q.reshape(Nq, nheads, D).transpose(1, 0, 2)
-    ak = avg_k.reshape(Nk, nheads, D).transpose(1, 0, 2)
-    scores = aq @ ak.transpose(0, 2, 1) / math.sqrt(D)
+    per (head, query time row) (lcsa/reference.py:37-64).  Returns [h,Nq,Nk]
+    bool (and the attn map with ``return_attn``).
+
+    q_w/k_w [N, 128, h*d] as float32 values follow torch's float32 run of those
+    lines.  As uint16 bf16 bits they follow its bf16 run, where every stage is
+    rounded to bf16: mean = bf16(fp32 sum * 2^-7) (reference.py:41-42),
+    einsum = bf16(fp32 dot) then ``/ math.sqrt(D)`` = bf16(s * fp32(1/fp32(sqrt
+    D))), the reciprocal form the GPU division by a scalar takes (:47),
+    -inf outside the tiled local mask (:49-55), softmax = bf16(fp32 exp(s -
+    max) / fp32 sum) (:57).  The bf16 run's sums are taken in float64 (exact
+    for bf16 data of ordinary range) and rounded once."""
+    local = np.asarray(local, bool)
     sq, sk = local.shape
-    rl, rn = Nq // sq, Nk // sk
-    lm = np.tile(local, (rl, rn))
-    scores = np.where(lm[None], scores, -np.inf)
-    scores = scores - scores.max(-1, keepdims=True)
-    e = np.exp(scores)
-    attn = e / e.sum(-1, keepdims=True)
+    if np.asarray(q_w).dtype == np.uint16:
+        q = from_bf16_bits(q_w).astype(np.float64)
+        k = from_bf16_bits(k_w).astype(np.float64)
+        avg_q = bf16(q.sum(1).astype(np.float32) * np.float32(2.0 ** -7))
+        avg_k = bf16(k.sum(1).astype(np.float32) * np.float32(2.0 ** -7))
+        Nq, HD = avg_q.shape
+        Nk = avg_k.shape[0]
+        D = HD // nheads
+        aq = avg_q.reshape(Nq, nheads, D).transpose(1, 0, 2).astype(np.float64)
+        ak = avg_k.reshape(Nk, nheads, D).transpose(1, 0, 2).astype(np.float64)
+        raw = bf16((aq @ ak.transpose(0, 2, 1)).astype(np.float32))
+        inv = np.float32(1.0) / np.float32(math.sqrt(D))
+        scores = bf16(raw * inv)
+        scores = np.where(np.tile(local, (Nq // sq, Nk // sk))[None], scores,
+                          np.float32(-np.inf))
+        with np.errstate(invalid="ignore"):
+            d = scores - scores.max(-1, keepdims=True)
+            e = np.exp(d.astype(np.float64)).astype(np.float32)
+            tot = e.astype(np.float64).sum(-1, keepdims=True).astype(np.float32)
+            attn = bf16(e / tot)
+        attn = np.where(np.isnan(attn), from_bf16_bits(np.uint16(0x7FC0)), attn)
+    else:
+        avg_q = np.asarray(q_w, np.float32).mean(1)
+        avg_k = np.asarray(k_w, np.float32).mean(1)
+        Nq, HD = avg_q.shape
+        Nk = avg_k.shape[0]
+        D = HD // nheads
+        aq = avg_q.reshape(Nq, nheads, D).transpose(1, 0, 2)
+        ak = avg_k.reshape(Nk, nheads, D).transpose(1, 0, 2)
+        scores = aq @ ak.transpose(0, 2, 1) / math.sqrt(D)
+        scores = np.where(np.tile(local, (Nq // sq, Nk // sk))[None], scores, -np.inf)
+        with np.errstate(invalid="ignore"):
+            scores = scores - scores.max(-1, keepdims=True)
+            e = np.exp(scores)
+            attn = (e / e.sum(-1, keepdims=True)).astype(np.float32)
     flat = attn.reshape(nheads * q_temporal, (Nq // q_temporal) * Nk)
-    apply_topk = min(flat.shape[1] - 1, topk)
-    thr = -np.sort(-flat, axis=1)[:, apply_topk][:, None]
-    keep = flat > thr
-    return keep.reshape(nheads, Nq, Nk)
+    keep = _topk_threshold_keep(flat, topk).reshape(nheads, Nq, Nk)
+    return (keep, attn) if return_attn else keep
 
 
 def c4_block_mask(heads: int = 12, time_rows: int = 2, bh: int = 6, bw: int = 11,

@@ -436,6 +436,94 @@ def test_block_index_vs_oracle(ops):
             assert np.array_equal(sel[h, i, :cnt[h, i]], rs[h, i, :cnt[h, i]])
 
 
+def _draft_check(ops, qb, kb, H, q_temporal, local, topk, q_map=None, k_map=None, qw=None,
+                 kw=None):
+    """Device draft mask (keep and the fused block index) against the oracle's
+    bf16 run of lcsa/reference.py:37-64: bit-exact by construction."""
+    from flashvsr_sm89_ops.lcsa import draft_index
+    qw = qb if qw is None else qw
+    kw = kb if kw is None else kw
+    ref = O.draft_block_mask(qw, kw, H, q_temporal, local, topk)
+    NQ, NK = ref.shape[1], ref.shape[2]
+    dq = dev_bf16(qb.reshape(-1, qb.shape[-1]))
+    dk = dev_bf16(kb.reshape(-1, kb.shape[-1]))
+    mq = None if q_map is None else torch.from_numpy(q_map).to(DEV)
+    mk = None if k_map is None else torch.from_numpy(k_map).to(DEV)
+    (sel, cnt, maxk), keep = draft_index(dq, dk, nheads=H, q_temporal=q_temporal,
+                                         local=torch.from_numpy(local), topk=topk, nq=NQ, nk=NK,
+                                         q_map=mq, k_map=mk, want_keep=True)
+    keep = keep.cpu().numpy()
+    bad = np.argwhere(keep != ref)
+    assert len(bad) == 0, f"{len(bad)} mismatches, first {bad[:5].tolist()}"
+    rs, rc, _ = O.build_csr(ref)
+    sel, cnt = sel.cpu().numpy(), cnt.cpu().numpy()
+    assert maxk == NK and np.array_equal(cnt, rc)
+    for h in range(H):
+        for i in range(NQ):
+            assert np.array_equal(sel[h, i, :cnt[h, i]], rs[h, i, :cnt[h, i]])
+    return ref
+
+
+def test_draft_mask_c4_raster_maps(ops):
+    """C4 geometry (12 heads, 6x11 blocks per time row, 2 time rows): q and k
+    in raster order read through the window token map, local range 7."""
+    from flashvsr_sm89_ops.block import window_token_map
+    H, D, f, h, w = 12, 128, 4, 48, 88
+    qr = rnd_bits((f * h * w, H * D), 21)
+    kr = rnd_bits((f * h * w, H * D), 22, scale=0.5)
+    tm = window_token_map(f, h, w).numpy()
+    local = O.build_local_block_mask(6, 11, 7)
+    qw = O.window_partition(qr.reshape(1, f, h, w, H * D))
+    kw = O.window_partition(kr.reshape(1, f, h, w, H * D))
+    for topk in (0, 7, int(132 * 66 * 0.3), 132 * 66):
+        keep = _draft_check(ops, qr, kr, H, 2, local, topk, q_map=tm, k_map=tm, qw=qw, kw=kw)
+        assert (keep.reshape(H, 2, -1).sum(-1) <= max(topk, 0)).all()
+
+
+def test_draft_mask_kv_cache_and_ties(ops):
+    """More key blocks than query blocks (KV cache rows join the joint top-k),
+    window-order rows, and inputs drawn from few values so many attn values tie
+    at the threshold."""
+    H, D = 4, 128
+    NQ, NK = 2 * 12, 4 * 12
+    rng = np.random.default_rng(23)
+    q = O.bf16_bits(rng.integers(-2, 3, (NQ, 128, H * D)).astype(np.float32) * 0.25)
+    k = O.bf16_bits(rng.integers(-2, 3, (NK, 128, H * D)).astype(np.float32) * 0.25)
+    local = O.build_local_block_mask(3, 4, 3)
+    for topk in (1, 50, 300, 5000):
+        _draft_check(ops, q, k, H, 2, local, topk)
+    q2 = rnd_bits((NQ, 128, H * D), 24, scale=3.0)
+    _draft_check(ops, q2, rnd_bits((NK, 128, H * D), 25, scale=3.0), H, 1, local, 200)
+
+
+def test_draft_mask_empty_local_row(ops):
+    """A local row with no allowed key gives a NaN softmax row; torch.topk
+    orders NaN above every number and NaN > thr is false."""
+    H, D, NQ, NK = 2, 64, 12, 12
+    local = O.build_local_block_mask(3, 4, 3)
+    local[5, :] = False
+    q = rnd_bits((NQ, 128, H * D), 26)
+    k = rnd_bits((NK, 128, H * D), 27)
+    for topk in (3, 40, 70, 143):
+        _draft_check(ops, q, k, H, 1, local, topk)
+
+
+def test_draft_block_mask_reference_signature(ops):
+    """lcsa/reference.py:37-40 signature and the DiT call shape
+    (integrate.py:103-104), both returning bool masks."""
+    from flashvsr_sm89_ops.lcsa import draft_block_mask, generate_draft_block_mask
+    H = 2
+    q = rnd_bits((12, 128, 256), 28)
+    k = rnd_bits((12, 128, 256), 29)
+    local = O.build_local_block_mask(3, 4, 3)
+    ref = O.draft_block_mask(q, k, H, 1, local, 30)
+    got = draft_block_mask(dev_bf16(q), dev_bf16(k), H, 1, torch.from_numpy(local).to(DEV), 30)
+    assert got.dtype == torch.bool and np.array_equal(got.cpu().numpy(), ref)
+    got4 = generate_draft_block_mask(1, H, 1, dev_bf16(q), dev_bf16(k), topk=30,
+                                     local_attn_mask=torch.from_numpy(local).to(DEV))
+    assert got4.shape == (1, H, 12, 12) and np.array_equal(got4[0].cpu().numpy(), ref)
+
+
 def _attn_check(out, ref, tol=1e-2):
     err = np.abs(out - ref).max()
     assert err <= tol, f"max abs err {err}"

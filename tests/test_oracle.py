@@ -335,6 +335,71 @@ def test_local_and_draft_masks():
     assert (per_group <= 500).all()
 
 
+def test_draft_topk_threshold_brute_force():
+    """keep_i = v_i > (k+1)-th largest  <=>  v_i is a number and at most k values
+    (NaN counted as largest, torch.topk's order) are >= v_i."""
+    rng = np.random.default_rng(11)
+    for trial in range(200):
+        n = int(rng.integers(1, 30))
+        v = rng.integers(0, 6, (1, n)).astype(np.float32) / 8
+        v[rng.random((1, n)) < 0.1] = np.nan
+        topk = int(rng.integers(0, n + 3))
+        got = O._topk_threshold_keep(v, topk)[0]
+        k = min(n - 1, topk)
+        ge = lambda a, b: np.isnan(a) or (not np.isnan(b) and a >= b)
+        want = [not np.isnan(v[0, i]) and sum(ge(v[0, j], v[0, i]) for j in range(n)) <= k
+                for i in range(n)]
+        assert list(got) == want, (v, topk)
+
+
+def _torch_bf16_draft(qb, kb, nheads, q_temporal, local, topk):
+    """lcsa/reference.py:41-63 run by torch itself on bf16 CPU tensors."""
+    import torch
+    from einops import rearrange
+    tq = torch.from_numpy(O.from_bf16_bits(qb)).bfloat16()
+    tk = torch.from_numpy(O.from_bf16_bits(kb)).bfloat16()
+    aq = rearrange(torch.mean(tq, dim=1), "s (h d) -> h s d", h=nheads)
+    ak = rearrange(torch.mean(tk, dim=1), "s (h d) -> h s d", h=nheads)
+    scores = torch.einsum("hld,hmd->hlm", aq, ak) / math.sqrt(aq.shape[-1])
+    sq, sk = local.shape
+    lm = torch.from_numpy(local).unsqueeze(1).unsqueeze(0).repeat(
+        scores.shape[1] // sq, 1, scores.shape[2] // sk, 1)
+    lm = rearrange(lm, "x a y b -> (x a) (y b)")
+    scores = scores + torch.zeros_like(scores).masked_fill(~lm.unsqueeze(0), float("-inf"))
+    attn = torch.softmax(scores, dim=-1)
+    flat = rearrange(attn, "h (t s) m -> (h t) (s m)", t=q_temporal)
+    k = min(flat.shape[1] - 1, topk)
+    thr = torch.topk(flat, k=k + 1, dim=1, largest=True).values[:, -1].unsqueeze(1)
+    keep = rearrange(flat > thr, "(h t) (s m) -> h (t s) m", t=q_temporal,
+                     s=scores.shape[1] // q_temporal)
+    return keep.numpy(), attn.float().numpy()
+
+
+@pytest.mark.parametrize("seed,scale,empty_row", [(3, 2.0, False), (4, 0.05, False),
+                                                  (5, 1.0, True)])
+def test_draft_mask_bf16_matches_torch_bf16_run(seed, scale, empty_row):
+    """The oracle's bf16 run against torch's own bf16 kernels on the CPU
+    (mean, einsum, scalar division, softmax, topk): every stage's rounding,
+    the NaN rows of an empty local row, and the threshold ties.  The float32
+    reading of the same lines differs, so the staging is what is pinned."""
+    rng = np.random.default_rng(seed)
+    H, D, Nq, Nk = 4, 128, 24, 36
+    qb = O.bf16_bits(rng.standard_normal((Nq, 128, H * D)).astype(np.float32) * scale)
+    kb = O.bf16_bits(rng.standard_normal((Nk, 128, H * D)).astype(np.float32) * scale)
+    local = O.build_local_block_mask(3, 4, 3)
+    if empty_row:
+        local[7, :] = False
+    for topk in (5, 60, 400):
+        keep, attn = O.draft_block_mask(qb, kb, H, 2, local, topk, return_attn=True)
+        tkeep, tattn = _torch_bf16_draft(qb, kb, H, 2, local, topk)
+        assert np.array_equal(np.isnan(attn), np.isnan(tattn))
+        assert np.array_equal(np.nan_to_num(attn), np.nan_to_num(tattn))
+        assert np.array_equal(keep, tkeep)
+    k32 = O.draft_block_mask(O.from_bf16_bits(qb), O.from_bf16_bits(kb), H, 2, local, 60)
+    if not empty_row and scale > 1:
+        assert not np.array_equal(k32, _torch_bf16_draft(qb, kb, H, 2, local, 60)[0])
+
+
 def test_window_partition_roundtrip_and_token_map():
     rng = np.random.default_rng(7)
     x = rng.standard_normal((1, 4, 16, 24, 3)).astype(np.float32)
