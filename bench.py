@@ -274,6 +274,38 @@ def components(torch, fv):
     out["C4_bsa"] = {"ms_per_layer": t4, "density": kept / (HEADS * 132 * 132),
                      "TFLOPs": fl4 / (t4 * 1e-3) / 1e12, "frac_bf16": fl4 / (t4 * 1e-3) / PEAK["bf16"],
                      "density_sweep": sweep}
+    del qkv
+
+    # Draft block mask + block index at the C5 geometry: q, k raster [16896, 1536]
+    # read through the window token map, local range 7 on the 6x11 block grid,
+    # 2 time rows, top-k 30% of a time row's 66 x 132 scores.
+    from flashvsr_sm89_ops.block import window_token_map
+    from flashvsr_sm89_ops.lcsa.masks import local_block_mask
+    NB = L // 128
+    ns = n_sets_for(2 * L * DIM * 2)
+    qd = [randn(L, DIM) for _ in range(ns)]
+    kd = [randn(L, DIM) for _ in range(ns)]
+    tm = window_token_map(4, 48, 88, device=dev)
+    loc = torch.from_numpy(local_block_mask(6, 11, 7)).to(dev, torch.uint8)
+    topk = int(0.3 * 66 * NB)
+    sel = torch.empty((HEADS, NB, NB), dtype=torch.int32, device=dev)
+    cnt = torch.empty((HEADS, NB), dtype=torch.int32, device=dev)
+    Ld = _lib.lib()
+    wn = Ld.fvsr_draft_workspace_floats(HEADS, HD, NB, NB)
+    wsd = torch.empty(wn, dtype=torch.float32, device=dev)
+    st = _lib.stream(wsd)
+
+    def draft(i):
+        _lib.check(Ld.fvsr_draft_block_mask(
+            qd[i].data_ptr(), DIM, tm.data_ptr(), kd[i].data_ptr(), DIM, tm.data_ptr(), HEADS, HD,
+            NB, NB, 2, loc.data_ptr(), 66, 66, topk, None, sel.data_ptr(), cnt.data_ptr(),
+            wsd.data_ptr(), wn, st), "draft")
+    t_d = timeit(torch, draft, ns, iters=50)
+    pool_bytes = 2 * L * DIM * 2
+    out["F1_draft_index"] = {"ms": t_d, "pool_MB": pool_bytes / 1e6,
+                             "GBps_pool_bytes": gbs(pool_bytes, t_d),
+                             "kept_frac": float(cnt.sum().item()) / (HEADS * NB * NB)}
+    del qd, kd
     return out
 
 

@@ -11,7 +11,7 @@
 //   keep = attn > thr.
 // Sums are taken in fp64, where they are exact for bf16 data of any realistic
 // range, then rounded once: the results do not depend on summation order.
-// Three launches (pool, scores+softmax, select), no host synchronisation.
+// Four launches (pool, scores+softmax, threshold, index), no host synchronisation.
 #include "common.h"
 
 namespace {
@@ -36,32 +36,47 @@ FVSR_DEV double wave_sum_f64(double v) {
 // avg[n][c] for the NQ query blocks (blockIdx.x < NQ) and the NK key blocks
 // (the rest): token j of block n is row map[n*128 + j] (n*128 + j without a
 // map), rows ts elements apart.  A workgroup covers 512 channels of one block:
-// lane g owns 8 channels, wave w adds tokens 32w..32w+31, and the four partial
-// fp64 sums meet in LDS.
-__global__ __launch_bounds__(kThreads) void pool_kernel(const uint16_t* __restrict__ q, int64_t qts,
-                                                        const int32_t* __restrict__ qmap,
-                                                        const uint16_t* __restrict__ k, int64_t kts,
-                                                        const int32_t* __restrict__ kmap, int64_t NQ,
-                                                        int64_t C, uint16_t* __restrict__ avg) {
-  __shared__ double part[3][8][64];
-  const bool is_q = blockIdx.x < NQ;
-  const int64_t n = is_q ? (int64_t)blockIdx.x : (int64_t)blockIdx.x - NQ;
+// lane g owns 8 channels, wave w adds tokens 32w..32w+31 in two batches of 16
+// (each batch's loads issued before its first add), and the four partial fp64
+// sums meet in LDS.  The (NQ + NK) * ceil(C/512) workgroups fit the
+// GPU in one round at the C5 shape.
+constexpr int kPoolWaves = 4;
+constexpr int kPoolBatch = 16;
+
+__global__ __launch_bounds__(kPoolWaves * 64) void pool_kernel(
+    const uint16_t* __restrict__ q, int64_t qts, const int32_t* __restrict__ qmap,
+    const uint16_t* __restrict__ k, int64_t kts, const int32_t* __restrict__ kmap, int64_t NQ,
+    int64_t C, uint16_t* __restrict__ avg) {
+  __shared__ double part[kPoolWaves - 1][8][64];
+  // The channel slices of one block are neighbours in dispatch order.
+  const int64_t ny = (C + 511) / 512;
+  const int64_t blk = blockIdx.x / ny, y = blockIdx.x % ny;
+  const bool is_q = blk < NQ;
+  const int64_t n = is_q ? blk : blk - NQ;
   const uint16_t* x = is_q ? q : k;
   const int64_t ts = is_q ? qts : kts;
   const int32_t* map = is_q ? qmap : kmap;
   const int g = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t c0 = ((int64_t)blockIdx.y * 64 + g) * 8;
+  const int64_t c0 = (y * 64 + g) * 8;
   const bool active = c0 < C;
   double acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (active) {
-#pragma unroll 8
-    for (int j = w * 32; j < w * 32 + 32; ++j) {
-      const int64_t tok = map ? (int64_t)map[n * kBlk + j] : n * kBlk + j;
-      const u32x4_t v = *(const u32x4_t*)(x + tok * ts + c0);
+#pragma unroll 1
+    for (int b = 0; b < kBlk / kPoolWaves / kPoolBatch; ++b) {
+      u32x4_t v[kPoolBatch];
+      const int64_t p0 = n * kBlk + (w * (kBlk / kPoolWaves) + b * kPoolBatch);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        acc[2 * i] += (double)bf_lo(v[i]);
-        acc[2 * i + 1] += (double)bf_hi(v[i]);
+      for (int j = 0; j < kPoolBatch; ++j) {
+        const int64_t tok = map ? (int64_t)map[p0 + j] : p0 + j;
+        v[j] = *(const u32x4_t*)(x + tok * ts + c0);
+      }
+#pragma unroll
+      for (int j = 0; j < kPoolBatch; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          acc[2 * i] += (double)bf_lo(v[j][i]);
+          acc[2 * i + 1] += (double)bf_hi(v[j][i]);
+        }
       }
     }
   }
@@ -78,7 +93,9 @@ __global__ __launch_bounds__(kThreads) void pool_kernel(const uint16_t* __restri
 #pragma unroll
       for (int b = 0; b < 2; ++b) {
         const int e = 2 * i + b;
-        const double s = acc[e] + part[0][e][g] + part[1][e][g] + part[2][e][g];
+        double s = acc[e];
+#pragma unroll
+        for (int u = 0; u < kPoolWaves - 1; ++u) s += part[u][e][g];
         h2[b] = bf16_bits((float)s * 0.0078125f);
       }
       o[i] = h2[0] | (h2[1] << 16);
@@ -88,62 +105,105 @@ __global__ __launch_bounds__(kThreads) void pool_kernel(const uint16_t* __restri
   }
 }
 
-// One (head h, query block l) per workgroup: the NK masked scores, then their
-// softmax, written as bf16 bits to attn[h][l][:].  A thread owns key blocks
-// m = tid, tid+256, ... and keeps its scores in LDS between the passes.
+// Four query blocks l0..l0+3 of one head h per workgroup.  Pass 1: thread m
+// (m = tid, tid+256, ...) forms the four masked scores of key block m, reading
+// each avg_k value once for the four dot products (query values as fp64 in
+// LDS, four 16-byte key loads kept in flight); pass 2: wave w takes row l0+w,
+// its maximum, exponentials and sum by wave reductions, and writes the
+// softmax as bf16 bits to attn[h][l0+w][:] and, for the threshold search, the
+// row's histogram of nonzero patterns by high byte to hist[h][l0+w][0..127]
+// (attn <= 1 or the NaN 0x7fc0, so the high byte is below 128).
+constexpr int kRowsPerScoreWg = 4;
+
 __global__ __launch_bounds__(kThreads) void score_softmax_kernel(
     const uint16_t* __restrict__ avg_q, const uint16_t* __restrict__ avg_k, int64_t H, int64_t D,
     int64_t NQ, int64_t NK, const uint8_t* __restrict__ local, int64_t sq, int64_t sk,
-    float inv_sqrt_d, uint16_t* __restrict__ attn) {
-  extern __shared__ float smem[];  // D query values, NK scores
-  __shared__ float redf[4];
-  __shared__ double redd[4];
-  float* aq = smem;
-  float* srow = smem + D;
-  const int64_t h = blockIdx.x / NQ, l = blockIdx.x % NQ;
+    float inv_sqrt_d, uint16_t* __restrict__ attn, uint16_t* __restrict__ hist) {
+  extern __shared__ double smem_d[];  // query values [4][D] (fp64), scores [4][NK] (fp32)
+  __shared__ int rh[kRowsPerScoreWg][128];
+  constexpr int R = kRowsPerScoreWg;
+  const int64_t groups = (NQ + R - 1) / R;
+  const int64_t h = blockIdx.x / groups, l0 = (blockIdx.x % groups) * R;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t C = H * D;
-  for (int64_t d = tid; d < D; d += kThreads) aq[d] = bf2f(avg_q[l * C + h * D + d]);
+  double* aq = smem_d;
+  float* srow = (float*)(smem_d + R * D);
+  for (int64_t i = tid; i < R * D; i += kThreads) {
+    const int64_t l = l0 + i / D;
+    aq[i] = l < NQ ? (double)bf2f(avg_q[l * C + h * D + i % D]) : 0.0;
+  }
+  for (int i = tid; i < R * 128; i += kThreads) rh[i / 128][i % 128] = 0;
   __syncthreads();
-  const uint8_t* lrow = local + (l % sq) * sk;
-  float mx = -__builtin_huge_valf();
+  const int64_t nch = D / 8;
   for (int64_t m = tid; m < NK; m += kThreads) {
-    const uint16_t* ak = avg_k + m * C + h * D;
-    double p = 0.0;
-    for (int64_t d0 = 0; d0 < D; d0 += 8) {
-      const u32x4_t v = *(const u32x4_t*)(ak + d0);
+    const u32x4_t* ak = (const u32x4_t*)(avg_k + m * C + h * D);
+    double p[R] = {};
+    auto chunk = [&](const u32x4_t& v, int64_t c) {
+      const double* a = aq + 8 * c;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p = __builtin_fma((double)aq[d0 + 2 * i], (double)bf_lo(v[i]), p);
-        p = __builtin_fma((double)aq[d0 + 2 * i + 1], (double)bf_hi(v[i]), p);
+        const double k0 = (double)bf_lo(v[i]), k1 = (double)bf_hi(v[i]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          p[r] = __builtin_fma(a[r * D + 2 * i], k0, p[r]);
+          p[r] = __builtin_fma(a[r * D + 2 * i + 1], k1, p[r]);
+        }
       }
+    };
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    u32x4_t v0 = ak[0], v1 = nch > 1 ? ak[1] : zero, v2 = nch > 2 ? ak[2] : zero,
+            v3 = nch > 3 ? ak[3] : zero;
+#pragma unroll 1
+    for (int64_t c = 0; c < nch; c += 4) {
+      chunk(v0, c);
+      if (c + 4 < nch) v0 = ak[c + 4];
+      if (c + 1 < nch) chunk(v1, c + 1);
+      if (c + 5 < nch) v1 = ak[c + 5];
+      if (c + 2 < nch) chunk(v2, c + 2);
+      if (c + 6 < nch) v2 = ak[c + 6];
+      if (c + 3 < nch) chunk(v3, c + 3);
+      if (c + 7 < nch) v3 = ak[c + 7];
     }
-    float s = bf16_val(bf16_val((float)p) * inv_sqrt_d);
-    if (!lrow[m % sk]) s = -__builtin_huge_valf();
-    srow[m] = s;
-    mx = fmaxf(mx, s);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const bool allowed = local[((l0 + r) % sq) * sk + m % sk] != 0;
+      srow[r * NK + m] =
+          allowed ? bf16_val(bf16_val((float)p[r]) * inv_sqrt_d) : -__builtin_huge_valf();
+    }
   }
-  mx = wave_max(mx);
-  if (lane == 0) redf[wave] = mx;
   __syncthreads();
-  mx = fmaxf(fmaxf(redf[0], redf[1]), fmaxf(redf[2], redf[3]));
-  double sum = 0.0;
-  for (int64_t m = tid; m < NK; m += kThreads) {
-    const float e = (float)exp((double)(srow[m] - mx));
-    srow[m] = e;
-    sum += (double)e;
+  const int64_t l = l0 + wave;
+  if (l < NQ) {
+    float* row = srow + wave * NK;
+    float mx = -__builtin_huge_valf();
+    for (int64_t m = lane; m < NK; m += 64) mx = fmaxf(mx, row[m]);
+    mx = wave_max(mx);
+    double sum = 0.0;
+    for (int64_t m = lane; m < NK; m += 64) {
+      const float e = (float)exp((double)(row[m] - mx));
+      row[m] = e;
+      sum += (double)e;
+    }
+    const float tot = (float)wave_sum_f64(sum);
+    uint16_t* arow = attn + (h * NQ + l) * NK;
+    for (int64_t m = lane; m < NK; m += 64) {
+      const uint32_t b = bf16_bits(row[m] / tot);
+      arow[m] = (uint16_t)b;
+      if (b != 0u) atomicAdd(&rh[wave][b >> 8], 1);
+    }
   }
-  sum = wave_sum_f64(sum);
-  if (lane == 0) redd[wave] = sum;
   __syncthreads();
-  const float tot = (float)(redd[0] + redd[1] + redd[2] + redd[3]);
-  uint16_t* arow = attn + (h * NQ + l) * NK;
-  for (int64_t m = tid; m < NK; m += kThreads) arow[m] = (uint16_t)bf16_bits(srow[m] / tot);
+  if (l < NQ) {
+    uint16_t* hrow = hist + (h * NQ + l) * 128;
+    hrow[lane] = (uint16_t)rh[wave][lane];
+    hrow[lane + 64] = (uint16_t)rh[wave][lane + 64];
+  }
 }
 
-// Of the 256 bins hist[0..255], the largest b with sum(hist[b..255]) >= r,
-// and r minus sum(hist[b+1..255]).  Run by wave 0; the answer goes to out[0..1].
-FVSR_DEV void find_bin(const int* hist, int r, int* out) {
+// Of the 256 bins hist[0..255] (in LDS), the largest b with sum(hist[b..255])
+// >= r, and r minus sum(hist[b+1..255]); b = -1 if the total is below r.  Run
+// by one whole wave; every lane returns the answer.
+FVSR_DEV int2 find_bin(const int* hist, int r) {
   const int lane = threadIdx.x & 63;
   int c[4], lsum = 0;
 #pragma unroll
@@ -151,79 +211,131 @@ FVSR_DEV void find_bin(const int* hist, int r, int* out) {
     c[i] = hist[lane * 4 + i];
     lsum += c[i];
   }
-  int suf = lsum;  // becomes sum over lanes >= lane
+  int suf = lsum;  // becomes the sum over lanes >= lane
   for (int o = 1; o < 64; o <<= 1) {
     const int t = __shfl_down(suf, o, 64);
     if (lane + o < 64) suf += t;
   }
   const uint64_t ok = __ballot(suf >= r);
+  if (!ok) return make_int2(-1, r);
   const int top = 63 - __clzll(ok);
+  int bin = 0, rest = 0;
   if (lane == top) {
     int above = suf - lsum;  // bins of higher lanes
     int b = 3;
     while (above + c[b] < r) above += c[b--];
-    out[0] = lane * 4 + b;
-    out[1] = r - above;
+    bin = lane * 4 + b;
+    rest = r - above;
   }
+  return make_int2(__shfl(bin, top, 64), __shfl(rest, top, 64));
 }
 
-// One (head, query time row) per workgroup.  The slab attn[h][t*S .. t*S+S)[:]
-// (S = NQ / q_temporal) is contiguous.  The threshold is the (k+1)-th largest
-// bf16 pattern (k = min(topk, S*NK - 1); attn is non-negative or the NaN
-// 0x7fc0, so patterns order like values with NaN largest), found by two
-// 256-bin histogram passes over the high and low bytes.  keep = attn > thr as
-// floats; sel/cnt (if given) list each row's kept key blocks ascending.
-__global__ __launch_bounds__(kThreads) void select_kernel(const uint16_t* __restrict__ attn,
-                                                          int64_t NQ, int64_t NK, int64_t q_temporal,
-                                                          int64_t topk, uint8_t* __restrict__ keep,
-                                                          int32_t* __restrict__ sel,
-                                                          int32_t* __restrict__ cnt) {
-  __shared__ int hist[256];
-  __shared__ int pick[2];
+// One (head, query time row) per workgroup: the threshold pattern of the
+// joint top-k over the slab attn[h][t*S .. t*S+S)[:] (S = NQ / q_temporal,
+// n = S*NK values), the (k+1)-th largest pattern with k = min(topk, n - 1).
+// attn is non-negative or the NaN 0x7fc0, so patterns order like values with
+// NaN largest, as torch.topk orders them.  Zeros (the masked blocks) are left
+// out of the histograms: if fewer than k+1 values are nonzero the threshold is
+// 0.  Otherwise the rows' high-byte histograms give the threshold's high byte
+// and its rank r2 among the values sharing it; one pass over the slab then
+// builds the low-byte histogram of those values in LDS.
+constexpr int kSelPer = 16;
+
+__global__ __launch_bounds__(kThreads) void threshold_kernel(const uint16_t* __restrict__ attn,
+                                                             const uint16_t* __restrict__ hist,
+                                                             int64_t NQ, int64_t NK,
+                                                             int64_t q_temporal, int64_t topk,
+                                                             uint32_t* __restrict__ thr) {
+  __shared__ int bins[256];
+  __shared__ int upper[128];
+  __shared__ int2 pick;
   const int64_t h = blockIdx.x / q_temporal, t = blockIdx.x % q_temporal;
   const int64_t S = NQ / q_temporal, n = S * NK;
-  const int64_t off = (h * NQ + t * S) * NK;
-  const uint16_t* vals = attn + off;
   const int tid = threadIdx.x;
   const int r = (int)((topk < n - 1 ? topk : n - 1) + 1);
 
-  hist[tid] = 0;
+  // High-byte totals: thread tid sums bin tid % 128 over rows of parity tid / 128.
+  const uint16_t* hs = hist + (h * NQ + t * S) * 128;
+  int c = 0;
+  for (int64_t r0 = tid >> 7; r0 < S; r0 += 16) {
+    uint32_t x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = r0 + 2 * u < S ? hs[(r0 + 2 * u) * 128 + (tid & 127)] : 0u;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) c += (int)x[u];
+  }
+  if (tid >= 128) upper[tid - 128] = c;
   __syncthreads();
-  for (int64_t i = tid; i < n; i += kThreads) atomicAdd(&hist[vals[i] >> 8], 1);
+  if (tid < 128) bins[tid] = c + upper[tid];
+  else bins[tid] = 0;
   __syncthreads();
-  if (tid < 64) find_bin(hist, r, pick);
-  __syncthreads();
-  const uint32_t hi = (uint32_t)pick[0];
-  const int r2 = pick[1];
-  __syncthreads();
-  hist[tid] = 0;
-  __syncthreads();
-  for (int64_t i = tid; i < n; i += kThreads) {
-    const uint32_t v = vals[i];
-    if ((v >> 8) == hi) atomicAdd(&hist[v & 0xff], 1);
+  if (tid < 64) {
+    const int2 f = find_bin(bins, r);
+    if (tid == 0) pick = f;
   }
   __syncthreads();
-  if (tid < 64) find_bin(hist, r2, pick);
+  const int hb = pick.x, r2 = pick.y;
+  if (hb < 0) {  // fewer than k+1 nonzero values: the threshold is 0
+    if (tid == 0) thr[blockIdx.x] = 0u;
+    return;
+  }
+  bins[tid] = 0;
   __syncthreads();
-  const float thr = __uint_as_float(((hi << 8) | (uint32_t)pick[0]) << 16);
+  const uint16_t* vals = attn + (h * NQ + t * S) * NK;
+  for (int64_t base = 0; base < n; base += kSelPer * kThreads) {
+    uint32_t v[kSelPer];
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i) {
+      const int64_t idx = base + i * kThreads + tid;
+      v[i] = idx < n ? (uint32_t)vals[idx] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kSelPer; ++i)
+      if (v[i] != 0u && (int)(v[i] >> 8) == hb) atomicAdd(&bins[v[i] & 0xff], 1);
+  }
+  __syncthreads();
+  if (tid < 64) {
+    const int2 f = find_bin(bins, r2);
+    if (tid == 0) thr[blockIdx.x] = ((uint32_t)hb << 8) | (uint32_t)f.x;
+  }
+}
 
-  if (keep)
-    for (int64_t i = tid; i < n; i += kThreads) keep[off + i] = bf2f(vals[i]) > thr ? 1 : 0;
-  if (sel) {
-    const int lane = tid & 63;
-    for (int64_t row = tid >> 6; row < S; row += kThreads / 64) {
-      const uint16_t* ar = vals + row * NK;
-      int32_t* sr = sel + off + row * NK;
-      int base = 0;
-      for (int64_t c0 = 0; c0 < NK; c0 += 64) {
-        const bool f = c0 + lane < NK && bf2f(ar[c0 + lane]) > thr;
+// One row (h, l) per wave: keep = attn > thr (as floats, so the NaN threshold
+// keeps nothing) and/or the row's kept key blocks ascending in sel, count in cnt.
+__global__ __launch_bounds__(kThreads) void index_kernel(const uint16_t* __restrict__ attn,
+                                                         const uint32_t* __restrict__ thr,
+                                                         int64_t rows, int64_t NQ, int64_t NK,
+                                                         int64_t q_temporal,
+                                                         uint8_t* __restrict__ keep,
+                                                         int32_t* __restrict__ sel,
+                                                         int32_t* __restrict__ cnt) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t h = row / NQ, l = row % NQ, S = NQ / q_temporal;
+  const float th = bf2f((uint16_t)thr[h * q_temporal + l / S]);
+  const uint16_t* ar = attn + row * NK;
+  int base = 0;
+  for (int64_t c0 = 0; c0 < NK; c0 += 8 * 64) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t m = c0 + u * 64 + lane;
+      v[u] = m < NK ? (uint32_t)ar[m] : 0u;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t m = c0 + u * 64 + lane;
+      const bool f = m < NK && bf2f((uint16_t)v[u]) > th;
+      if (keep && m < NK) keep[row * NK + m] = f ? 1 : 0;
+      if (sel) {
         const uint64_t bal = __ballot(f);
-        if (f) sr[base + __popcll(bal & ((1ull << lane) - 1ull))] = (int32_t)(c0 + lane);
+        if (f) sel[row * NK + base + __popcll(bal & ((1ull << lane) - 1ull))] = (int32_t)m;
         base += __popcll(bal);
       }
-      if (lane == 0) cnt[h * NQ + t * S + row] = base;
     }
   }
+  if (sel && lane == 0) cnt[row] = base;
 }
 
 constexpr int64_t align64(int64_t n) { return (n + 63) & ~(int64_t)63; }
@@ -232,8 +344,12 @@ constexpr int64_t align64(int64_t n) { return (n + 63) & ~(int64_t)63; }
 
 extern "C" int64_t fvsr_draft_workspace_floats(int64_t H, int64_t D, int64_t NQ, int64_t NK) {
   if (H <= 0 || D <= 0 || NQ < 0 || NK < 0) return 0;
-  // bf16 avg_q [NQ, H*D], avg_k [NK, H*D] and attn [H, NQ, NK], 256-byte aligned.
-  return (align64((NQ + NK) * H * D) + align64(H * NQ * NK)) / 2 + 64;
+  // In 16-bit units, each region 128-byte aligned: bf16 avg_q [NQ, H*D] and
+  // avg_k [NK, H*D], bf16 attn [H, NQ, NK], uint16 hist [H, NQ, 128] and the
+  // uint32 thresholds [H * q_temporal] (at most H * NQ); + 256 bytes of slack.
+  const int64_t units = align64((NQ + NK) * H * D) + align64(H * NQ * NK) +
+                        align64(H * NQ * 128) + align64(2 * H * NQ);
+  return units / 2 + 64;
 }
 
 extern "C" int fvsr_draft_block_mask(const void* q, int64_t q_tok_stride, const int32_t* q_map,
@@ -253,22 +369,28 @@ extern "C" int fvsr_draft_block_mask(const void* q, int64_t q_tok_stride, const 
       ((uintptr_t)workspace & 15))
     return FVSR_EUNSUPPORTED;
   if (workspace_floats < fvsr_draft_workspace_floats(H, D, NQ, NK)) return FVSR_EWORKSPACE;
-  // LDS holds D + NK floats; the select pass counts a slab in int.
-  if (D + NK > 12288 || (NQ / q_temporal) * NK > 0x7fffffff || H * NQ > 0x7fffffff ||
-      NQ + NK > 0x7fffffff)
+  // LDS holds 4 * D doubles and 4 * NK floats (at most 62 KB).
+  if (2 * D + NK > 3968 || (NQ / q_temporal) * NK > 0x7fffffff || H * NQ > 0x7fffffff ||
+      (NQ + NK) * ((H * D + 511) / 512) > 0x7fffffff)
     return FVSR_EUNSUPPORTED;
   hipStream_t st = (hipStream_t)stream;
   const int64_t C = H * D;
   uint16_t* avg = (uint16_t*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
   uint16_t* attn = avg + align64((NQ + NK) * C);
-  hipLaunchKernelGGL(pool_kernel, dim3((unsigned)(NQ + NK), (unsigned)((C + 511) / 512)),
-                     dim3(kThreads), 0, st, (const uint16_t*)q, q_tok_stride, q_map,
+  hipLaunchKernelGGL(pool_kernel, dim3((unsigned)((NQ + NK) * ((C + 511) / 512))),
+                     dim3(kPoolWaves * 64), 0, st, (const uint16_t*)q, q_tok_stride, q_map,
                      (const uint16_t*)k, k_tok_stride, k_map, NQ, C, avg);
   const float inv_sqrt_d = 1.0f / (float)sqrt((double)D);
-  hipLaunchKernelGGL(score_softmax_kernel, dim3((unsigned)(H * NQ)), dim3(kThreads),
-                     (D + NK) * sizeof(float), st, avg, avg + NQ * C, H, D, NQ, NK, local, sq, sk,
-                     inv_sqrt_d, attn);
-  hipLaunchKernelGGL(select_kernel, dim3((unsigned)(H * q_temporal)), dim3(kThreads), 0, st, attn,
-                     NQ, NK, q_temporal, topk, keep, sel, cnt);
+  uint16_t* hist = attn + align64(H * NQ * NK);
+  uint32_t* thr = (uint32_t*)(hist + align64(H * NQ * 128));
+  const int64_t groups = (NQ + kRowsPerScoreWg - 1) / kRowsPerScoreWg;
+  hipLaunchKernelGGL(score_softmax_kernel, dim3((unsigned)(H * groups)), dim3(kThreads),
+                     kRowsPerScoreWg * (D * sizeof(double) + NK * sizeof(float)), st, avg,
+                     avg + NQ * C, H, D, NQ, NK, local, sq, sk, inv_sqrt_d, attn, hist);
+  hipLaunchKernelGGL(threshold_kernel, dim3((unsigned)(H * q_temporal)), dim3(kThreads), 0, st,
+                     attn, hist, NQ, NK, q_temporal, topk, thr);
+  const int64_t rows = H * NQ;
+  hipLaunchKernelGGL(index_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kThreads), 0, st, attn,
+                     thr, rows, NQ, NK, q_temporal, keep, sel, cnt);
   return fvsr_launch_status();
 }

@@ -178,7 +178,7 @@ int64_t fvsr_draft_workspace_floats(int64_t H, int64_t D, int64_t NQ, int64_t NK
  * cnt int32 [H, NQ] in fvsr_block_index's form (kept block ids ascending).
  * workspace: fvsr_draft_workspace_floats(H, D, NQ, NK).
  * Requires D % 8 == 0, token strides % 8 == 0, 16-byte aligned q and k, and
- * D + NK <= 12288.
+ * 2*D + NK <= 3968.
  */
 int fvsr_draft_block_mask(const void* q, int64_t q_tok_stride, const int32_t* q_map,
                           const void* k, int64_t k_tok_stride, const int32_t* k_map, int64_t H,

@@ -508,6 +508,19 @@ def test_draft_mask_empty_local_row(ops):
         _draft_check(ops, q, k, H, 1, local, topk)
 
 
+def test_draft_mask_dense_local_in_place_search(ops):
+    """An all-true local rule leaves no zero in the softmax, and one time row
+    of 132 x 132 blocks holds more nonzero values than the select kernel
+    gathers in LDS: the threshold search then runs over the slab in place."""
+    H, D, NQ, NK = 2, 64, 132, 132
+    local = np.ones((66, 66), bool)
+    q = rnd_bits((NQ, 128, H * D), 30)
+    k = rnd_bits((NK, 128, H * D), 31)
+    for topk in (100, 5000, 17423):
+        _draft_check(ops, q, k, H, 1, local, topk)
+    _draft_check(ops, q, k, H, 2, local, 3000)
+
+
 def test_draft_block_mask_reference_signature(ops):
     """lcsa/reference.py:37-40 signature and the DiT call shape
     (integrate.py:103-104), both returning bool masks."""
