@@ -70,9 +70,9 @@ def block_costs():
     """Algorithmic work per DiT block (per launch of each op)."""
     gem = {
         "gemm_qkv": 2 * L * DIM * 3 * DIM,
-        "gemm_o_gate": 2 * L * DIM * DIM,
+        "gemm_o": 2 * L * DIM * DIM,
         "gemm_ffn0": 2 * L * DIM * FFN,
-        "gemm_ffn2_gate": 2 * L * FFN * DIM,
+        "gemm_ffn2": 2 * L * FFN * DIM,
     }
     return gem
 
@@ -236,10 +236,15 @@ def components(torch, fv):
     hq, hsc = fv.fused_gelu_quant_fp8(hs_[0], per_token=True)
     res = xs[0].view(M3, DIM)
     o2 = torch.empty((M3, DIM), dtype=torch.bfloat16, device=dev)
-    t_g2 = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2, epilogue=_lib.EPI_GATE_ADD,
-                                               res=res, gate=gt.view(DIM)), 1)
+    t_g2 = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2), 1)
+    t_g2g = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2, epilogue=_lib.EPI_GATE_ADD,
+                                                res=res, gate=gt.view(DIM)), 1)
     t_ga = timeit(torch, lambda i: fv.fused_gate_add(xs[i], gt, xs[(i + 1) % ns]), ns)
     ga_bytes = M3 * DIM * 6 + DIM * 2
+    from flashvsr_sm89_ops.fused_adaln import fused_gate_add_ln_modulate_quant
+    t_gal = timeit(torch, lambda i: fused_gate_add_ln_modulate_quant(
+        xs[i], gt, xs[(i + 1) % ns], sc, sh), ns)
+    gal_bytes = M3 * DIM * (2 + 2 + 2 + 1) + M3 * 4 + 4 * DIM * 2
     t_ffn = timeit(torch, lambda i: (lambda h8: fv.fp8_gemm(h8[0], h8[1], w2, s2, b2))(
         gemm_gelu_quant_fp8(x8s[i % 2][0], x8s[i % 2][1], lin1, True)), 2)
     fl = 2 * M3 * DIM * FFN
@@ -250,10 +255,14 @@ def components(torch, fv):
         "gemm_ffn0_ms": t_g1, "gemm_ffn0_TFLOPs": fl / (t_g1 * 1e-3) / 1e12,
         "gemm_ffn0_frac_fp8": fl / (t_g1 * 1e-3) / PEAK["fp8"],
         "gelu_quant_ms": t_rq, "gelu_quant_GBps": gbs(rq_bytes, t_rq),
-        "gemm_ffn2_gate_ms": t_g2, "gemm_ffn2_gate_TFLOPs": fl / (t_g2 * 1e-3) / 1e12,
-        "gemm_ffn2_gate_frac_fp8": fl / (t_g2 * 1e-3) / PEAK["fp8"],
+        "gemm_ffn2_ms": t_g2, "gemm_ffn2_TFLOPs": fl / (t_g2 * 1e-3) / 1e12,
+        "gemm_ffn2_frac_fp8": fl / (t_g2 * 1e-3) / PEAK["fp8"],
+        "gemm_ffn2_gate_epilogue_ms": t_g2g,
         "gate_add_ms": t_ga, "gate_add_GBps": gbs(ga_bytes, t_ga),
         "gate_add_frac_hbm": gbs(ga_bytes, t_ga) * 1e9 / PEAK["hbm"],
+        "gate_add_ln_modulate_quant_ms": t_gal,
+        "gate_add_ln_modulate_quant_GBps": gbs(gal_bytes, t_gal),
+        "gate_add_ln_modulate_quant_frac_hbm": gbs(gal_bytes, t_gal) * 1e9 / PEAK["hbm"],
         "ffn_chain_ms": t_ffn}
     del xs, x8s, hs_, hq, hb
 
@@ -306,6 +315,25 @@ def components(torch, fv):
                              "GBps_pool_bytes": gbs(pool_bytes, t_d),
                              "kept_frac": float(cnt.sum().item()) / (HEADS * NB * NB)}
     del qd, kd
+
+    # F3: x + cross_attn(norm3(x)) at the C5 shape, prompt K/V of 512 tokens
+    # (LayerNorm+quant, FP8 q, RMSNorm, dense attention, quant, FP8 o + residual).
+    from flashvsr_sm89_ops.block import DiTBlockWeights
+    from flashvsr_sm89_ops.cross_attn import cross_attention, cross_attention_residual
+    LK = 512
+    c = DiTBlockWeights(DIM, FFN, dev, torch.Generator().manual_seed(1), cross_len=LK).cross
+    ns = n_sets_for(L * DIM * 2)
+    xs = [randn(1, L, DIM) for _ in range(ns)]
+    t_x = timeit(torch, lambda i: cross_attention_residual(
+        xs[i], c["norm3_w"], c["norm3_b"], c["q"], c["norm_q"], c["k"], c["v"], c["o"], HEADS), ns)
+    t_a = timeit(torch, lambda i: cross_attention(xs[i], c["k"], c["v"], HEADS), ns)
+    fl_a = 4 * L * LK * DIM
+    fl_g = 2 * 2 * L * DIM * DIM
+    out["F3_cross_attn"] = {"ms": t_x, "prompt_tokens": LK, "attn_ms": t_a,
+                            "attn_TFLOPs": fl_a / (t_a * 1e-3) / 1e12,
+                            "attn_frac_bf16": fl_a / (t_a * 1e-3) / PEAK["bf16"],
+                            "gemm_GFLOP": fl_g / 1e9, "attn_GFLOP": fl_a / 1e9}
+    del xs
     return out
 
 

@@ -81,11 +81,17 @@ FVSR_DEV bool ln_fast_ok(float mean, float rd) {
 // all R rows are loaded before any arithmetic, so each wave keeps R row loads
 // in flight.  Row groups never straddle a batch element; a group running
 // past the batch's last row recomputes that row and stores nothing for it.
-template <int VPL, int R, bool WRITE_OUT, bool QUANT>
+//
+// GATE: the row is first formed as x1 = bf16(x + bf16(gate * res)) (the
+// gated residual of the op before, fused_gate_add's arithmetic) and written
+// to x1_out; the LayerNorm then runs on x1 from registers.
+template <int VPL, int R, bool WRITE_OUT, bool QUANT, bool GATE = false>
 __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
     const uint16_t* __restrict__ shift, uint16_t* __restrict__ out, int64_t B, int64_t L,
-    int64_t D, float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
+    int64_t D, float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale,
+    const uint16_t* __restrict__ gate = nullptr, const uint16_t* __restrict__ res = nullptr,
+    uint16_t* __restrict__ x1_out = nullptr) {
   const int lane = threadIdx.x & 63;
   const int64_t groups = (L + R - 1) / R;
   const int64_t g = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
@@ -111,6 +117,31 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
     const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
     sraw[j] = *(const u32x4_t*)(scale + pb + cc * 8);
     shraw[j] = *(const u32x4_t*)(shift + pb + cc * 8);
+  }
+  if (GATE) {
+    u32x4_t rraw[R][VPL], graw[VPL];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j)
+        rraw[r][j] = *(const u32x4_t*)(res + row[r] * D + clamp_chunk(lane + 64 * j, nchunk) * 8);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      graw[j] = *(const u32x4_t*)(gate + pb + clamp_chunk(lane + 64 * j, nchunk) * 8);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t t = pack_bf16x2_once(bf_lo(graw[j][p]) * bf_lo(rraw[r][j][p]),
+                                              bf_hi(graw[j][p]) * bf_hi(rraw[r][j][p]));
+          raw[r][j][p] = pack_bf16x2_once(bf_lo(raw[r][j][p]) + bf_lo(t),
+                                          bf_hi(raw[r][j][p]) + bf_hi(t));
+        }
+        const int64_t c = lane + 64 * j;
+        if (c < nchunk && l0 + r < L) *(u32x4_t*)(x1_out + row[r] * D + c * 8) = raw[r][j];
+      }
   }
   float v[R][VPL][8], sum[R];
 #pragma unroll
@@ -248,6 +279,132 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_generic(
   }
 }
 
+// LayerNorm with affine weight and bias (the DiT block's norm3 before the
+// cross-attention), in torch's arithmetic for bf16 tensors: mean and variance
+// in fp32, y = bf16(w * ((x - mean) * rstd) + b) in fp32 with
+// rstd = rsqrt(var + eps), one rounding.  R rows per wavefront, rows in
+// registers as in ln_modulate_vec; optional per-row e4m3 codes of y.
+template <int VPL, int R, bool WRITE_OUT, bool QUANT>
+__global__ __launch_bounds__(kThreads) void layer_norm_vec(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t rows, int64_t D,
+    float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = ((int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
+  if (r0 >= rows) return;
+  const int64_t nchunk = D >> 3;
+  int64_t row[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) row[r] = r0 + r < rows ? r0 + r : rows - 1;
+  u32x4_t raw[R][VPL], wraw[VPL], braw[VPL];
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+      raw[r][j] = *(const u32x4_t*)(x + row[r] * D + clamp_chunk(lane + 64 * j, nchunk) * 8);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
+    wraw[j] = *(const u32x4_t*)(w + cc * 8);
+    braw[j] = *(const u32x4_t*)(bias + cc * 8);
+  }
+  float v[R][VPL][8], sum[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    sum[r] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      unpack8(raw[r][j], v[r][j]);
+      float cs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) cs += v[r][j][e];
+      sum[r] += lane + 64 * j < nchunk ? cs : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const float mean = wave_sum(sum[r]) / (float)D;
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      float cs = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[r][j][e] -= mean;
+        cs = __builtin_fmaf(v[r][j][e], v[r][j][e], cs);
+      }
+      sq += lane + 64 * j < nchunk ? cs : 0.0f;
+    }
+    const float rstd = rsqrtf(wave_sum(sq) / (float)D + eps);
+    u32x4_t o[VPL];
+    u16x2_t mx = {0, 0};
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float y0 = __builtin_fmaf(bf_lo(wraw[j][p]), v[r][j][2 * p] * rstd, bf_lo(braw[j][p]));
+        const float y1 =
+            __builtin_fmaf(bf_hi(wraw[j][p]), v[r][j][2 * p + 1] * rstd, bf_hi(braw[j][p]));
+        o[j][p] = pack_bf16x2_once(y0, y1);
+        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, o[j][p] & 0x7fff7fffu));
+      }
+      const int64_t c = lane + 64 * j;
+      if (WRITE_OUT && c < nchunk && r0 + r < rows) *(u32x4_t*)(out + row[r] * D + c * 8) = o[j];
+    }
+    if (QUANT) {
+      const float amax = wave_max_abs(fmaxf(bf2f(mx[0]), bf2f(mx[1])));
+      const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t c = lane + 64 * j;
+        if (c < nchunk && r0 + r < rows) {
+          u32x2_t q;
+          q[0] = e4m3x4_div(bf_lo(o[j][0]), bf_hi(o[j][0]), bf_lo(o[j][1]), bf_hi(o[j][1]), qs, qr);
+          q[1] = e4m3x4_div(bf_lo(o[j][2]), bf_hi(o[j][2]), bf_lo(o[j][3]), bf_hi(o[j][3]), qs, qr);
+          *(u32x2_t*)(codes + row[r] * D + c * 8) = q;
+        }
+      }
+      if (lane == 0 && r0 + r < rows) row_scale[row[r]] = amax / 448.0f;
+    }
+  }
+}
+
+// Any D: passes over the row from global memory.
+__global__ __launch_bounds__(kThreads) void layer_norm_generic(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t rows, int64_t D,
+    float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * D;
+  float sum = 0.0f;
+  for (int64_t d = lane; d < D; d += 64) sum += bf2f(xr[d]);
+  const float mean = wave_sum(sum) / (float)D;
+  float sq = 0.0f;
+  for (int64_t d = lane; d < D; d += 64) {
+    const float t = bf2f(xr[d]) - mean;
+    sq = __builtin_fmaf(t, t, sq);
+  }
+  const float rstd = rsqrtf(wave_sum(sq) / (float)D + eps);
+  float amax = 0.0f;
+  for (int64_t d = lane; d < D; d += 64) {
+    const float o = round_bf16(__builtin_fmaf(bf2f(w[d]), (bf2f(xr[d]) - mean) * rstd, bf2f(bias[d])));
+    amax = fmaxf(amax, fabsf(o));
+    if (out) out[row * D + d] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffff);
+  }
+  if (codes) {
+    amax = wave_max(amax);
+    const float qs = fmaxf(amax, 1e-12f) / 448.0f;
+    for (int64_t d = lane; d < D; d += 64) {
+      const float o = round_bf16(__builtin_fmaf(bf2f(w[d]), (bf2f(xr[d]) - mean) * rstd, bf2f(bias[d])));
+      codes[row * D + d] =
+          (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(o / qs), 0.0f, 0, false) & 0xff);
+    }
+    if (lane == 0) row_scale[row] = amax / 448.0f;
+  }
+}
+
 constexpr int kGateUnroll = 2;
 
 __global__ __launch_bounds__(kThreads) void gate_add_vec(
@@ -328,6 +485,71 @@ extern "C" int fvsr_ln_modulate(const void* x, const void* scale, const void* sh
     hipLaunchKernelGGL(ln_modulate_generic, grid, block, 0, st, xp, sp, hp, op, rows, L, D, eps,
                        qp, row_scale);
   }
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_layer_norm(const void* x, const void* weight, const void* bias, void* out,
+                               int64_t rows, int64_t D, float eps, void* codes, float* row_scale,
+                               void* stream) {
+  if (rows < 0 || D <= 0) return FVSR_EINVAL;
+  if (rows == 0) return FVSR_OK;
+  if (!x || !weight || !bias || (!out && !codes) || (codes && !row_scale)) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *xp = (const uint16_t*)x, *wp = (const uint16_t*)weight,
+                 *bp = (const uint16_t*)bias;
+  uint16_t* op = (uint16_t*)out;
+  uint8_t* qp = (uint8_t*)codes;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(weight) &&
+                   aligned16(bias) && (!out || aligned16(out)) && (!codes || aligned16(codes));
+  if (vec) {
+    const int64_t groups = (rows + kLnRows - 1) / kLnRows;
+    const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves)), block(kThreads);
+    if (out && codes)
+      hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, true, true>), vgrid, block, 0, st, xp, wp,
+                         bp, op, rows, D, eps, qp, row_scale);
+    else if (out)
+      hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, true, false>), vgrid, block, 0, st, xp, wp,
+                         bp, op, rows, D, eps, qp, row_scale);
+    else
+      hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, false, true>), vgrid, block, 0, st, xp, wp,
+                         bp, op, rows, D, eps, qp, row_scale);
+  } else {
+    hipLaunchKernelGGL(layer_norm_generic, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
+                       dim3(kThreads), 0, st, xp, wp, bp, op, rows, D, eps, qp, row_scale);
+  }
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_gate_add_ln_modulate(const void* x, const void* gate, const void* res,
+                                         void* x1, const void* scale, const void* shift,
+                                         void* out, int64_t B, int64_t L, int64_t D, float eps,
+                                         void* codes, float* row_scale, void* stream) {
+  if (B < 0 || L < 0 || D <= 0) return FVSR_EINVAL;
+  if (B * L == 0) return FVSR_OK;
+  if (!x || !gate || !res || !x1 || !scale || !shift || (!out && !codes) ||
+      (codes && !row_scale))
+    return FVSR_EINVAL;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(gate) &&
+                   aligned16(res) && aligned16(x1) && aligned16(scale) && aligned16(shift) &&
+                   (!out || aligned16(out)) && (!codes || aligned16(codes));
+  if (!vec) return FVSR_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *xp = (const uint16_t*)x, *sp = (const uint16_t*)scale,
+                 *hp = (const uint16_t*)shift, *gp = (const uint16_t*)gate,
+                 *rp = (const uint16_t*)res;
+  uint16_t *op = (uint16_t*)out, *x1p = (uint16_t*)x1;
+  uint8_t* qp = (uint8_t*)codes;
+  const int64_t groups = B * ((L + kLnRows - 1) / kLnRows);
+  const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves)), block(kThreads);
+  if (out && codes)
+    hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, true, true, true>), vgrid, block, 0, st, xp, sp,
+                       hp, op, B, L, D, eps, qp, row_scale, gp, rp, x1p);
+  else if (out)
+    hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, true, false, true>), vgrid, block, 0, st, xp,
+                       sp, hp, op, B, L, D, eps, qp, row_scale, gp, rp, x1p);
+  else
+    hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, false, true, true>), vgrid, block, 0, st, xp,
+                       sp, hp, op, B, L, D, eps, qp, row_scale, gp, rp, x1p);
   return fvsr_launch_status();
 }
 

@@ -59,6 +59,7 @@ struct EpiArgs {
   const uint16_t* gate;
   int sa_row, sb_col;
   int vec_params;  // sb (per column) 16-byte aligned and bias 8-byte aligned
+  int res_vec;     // gate-add: N, ldc multiples of 8 and res / c / gate 16-byte aligned
 };
 
 FVSR_DEV void map_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -412,6 +413,19 @@ FVSR_DEV void epi_store(const uint16_t LDS_AS* stg, int64_t mw, int64_t nw, int6
                         const EpiArgs& e, int lane, int ip, int j, float (&vmax)[4]) {
   const int c8 = lane & 7;
   const int64_t n = nw + ip * 64 + c8 * 8;
+  // Gate-add with vector rows: the pass's four residual rows and its gate
+  // columns are loaded before any store (the stores may alias them when c ==
+  // res, which would otherwise order each load after the previous store).
+  u32x4_t rv[4], gv = {0u, 0u, 0u, 0u};
+  if (EPI == FVSR_EPI_GATE_ADD && e.res_vec) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int64_t m = mw + j * 32 + s * 8 + (lane >> 3);
+      const bool ok = m < M && n < N;
+      rv[s] = *(const u32x4_t*)(e.res + (ok ? m : 0) * e.ldc + (ok ? n : 0));
+    }
+    gv = *(const u32x4_t*)(e.gate + (n < N ? n : 0));
+  }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     const int row = s * 8 + (lane >> 3);
@@ -431,14 +445,12 @@ FVSR_DEV void epi_store(const uint16_t LDS_AS* stg, int64_t mw, int64_t nw, int6
       uint16_t* cp = e.c + m * e.ldc + n;
       if (EPI == FVSR_EPI_GATE_ADD) {
         const uint16_t* rp = e.res + m * e.ldc + n;
-        if (n + 7 < N && ((((uintptr_t)cp) | (uintptr_t)rp | (uintptr_t)(e.gate + n)) & 15) == 0) {
-          const u32x4_t rv = *(const u32x4_t*)rp;
-          const u32x4_t gv = *(const u32x4_t*)(e.gate + n);
+        if (e.res_vec) {
 #pragma unroll
           for (int w = 0; w < 4; ++w) {
             const float t0 = round_bf16(bf_lo(gv[w]) * bf_lo(v[w]));
             const float t1 = round_bf16(bf_hi(gv[w]) * bf_hi(v[w]));
-            v[w] = pack_bf16x2(bf_lo(rv[w]) + t0, bf_hi(rv[w]) + t1);
+            v[w] = pack_bf16x2(bf_lo(rv[s][w]) + t0, bf_hi(rv[s][w]) + t1);
           }
         } else {
 #pragma unroll
@@ -722,9 +734,11 @@ extern "C" int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa
   if (tiles > 0x7fffffff) return FVSR_EUNSUPPORTED;
   const int sb_col = sb_mode == FVSR_SCALE_ROW;
   const int vec_params = (!sb_col || ((uintptr_t)sb & 15) == 0) && ((uintptr_t)bias & 7) == 0;
+  const int res_vec = epilogue == FVSR_EPI_GATE_ADD && N % 8 == 0 && ldc % 8 == 0 &&
+                      ((((uintptr_t)res) | (uintptr_t)c | (uintptr_t)gate) & 15) == 0;
   EpiArgs ep{sa, sb, (const uint16_t*)bias, (uint16_t*)c, ldc, amax_part,
              fvsr_gemm_amax_parts(N), (const uint16_t*)res, (const uint16_t*)gate,
-             sa_mode == FVSR_SCALE_ROW, sb_col, vec_params};
+             sa_mode == FVSR_SCALE_ROW, sb_col, vec_params, res_vec};
   hipStream_t st = (hipStream_t)stream;
   // Persistent ring: K a multiple of 256, at least 8 K steps, and every row
   // offset of either operand within 32 bits.

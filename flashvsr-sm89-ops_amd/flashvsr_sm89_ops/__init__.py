@@ -12,12 +12,14 @@ from .compat_bsa import active_backend, ensure_bsa_available
 ensure_bsa_available()
 
 from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qk  # noqa: E402
-from .fused_adaln import fused_ln_modulate, fused_gate_add, fused_ln_modulate_quant  # noqa: E402
+from .fused_adaln import (fused_ln_modulate, fused_gate_add, fused_ln_modulate_quant,  # noqa: E402
+                          layer_norm, layer_norm_quant)
 from .fp8_quant import quantize_fp8, quantize_weight_fp8, FP8_MAX  # noqa: E402
 from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm  # noqa: E402
 from .fp8_ffn import FP8FFN, convert_ffn_fp8, fused_gelu_quant_fp8  # noqa: E402
 from .integrate import enable  # noqa: E402
-from .lcsa import block_sparse_attention, build_csr  # noqa: E402
+from .lcsa import block_sparse_attention, build_csr, draft_block_mask  # noqa: E402
+from .cross_attn import cross_attention, cross_attention_residual  # noqa: E402
 
 __version__ = "0.1.0"
 
@@ -28,6 +30,8 @@ __all__ = [
     "fused_ln_modulate",
     "fused_ln_modulate_quant",
     "fused_gate_add",
+    "layer_norm",
+    "layer_norm_quant",
     "quantize_fp8",
     "quantize_weight_fp8",
     "FP8_MAX",
@@ -39,6 +43,9 @@ __all__ = [
     "fused_gelu_quant_fp8",
     "block_sparse_attention",
     "build_csr",
+    "draft_block_mask",
+    "cross_attention",
+    "cross_attention_residual",
     "active_backend",
     "ensure_bsa_available",
 ]

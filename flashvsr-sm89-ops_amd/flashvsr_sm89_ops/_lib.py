@@ -43,6 +43,9 @@ _SIGS = {
     "fvsr_gemm_amax_parts": ([_I64], _I64),
     "fvsr_ln_modulate": ([_P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P], _I),
     "fvsr_gate_add": ([_P, _P, _P, _P, _I64, _I64, _I64, _P], _I),
+    "fvsr_layer_norm": ([_P, _P, _P, _P, _I64, _I64, _F, _P, _P, _P], _I),
+    "fvsr_gate_add_ln_modulate": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P],
+                                  _I),
     "fvsr_rms_rope": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P], _I),
     "fvsr_rms_rope_qk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I64, _I64,
                           _P], _I),

@@ -72,3 +72,72 @@ def fused_gate_add(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor):
                                         out.data_ptr(), B, L, D, _lib.stream(x)),
                "fused_gate_add")
     return out
+
+
+def _ln_affine_args(x, weight, bias):
+    _lib.require_gpu(x, weight, bias)
+    _lib.require_dtype(x, torch.bfloat16, "x")
+    D = x.shape[-1]
+    w = weight.to(torch.bfloat16).contiguous()
+    b = bias.to(torch.bfloat16).contiguous() if bias is not None else torch.zeros_like(w)
+    if w.numel() != D or b.numel() != D:
+        raise ValueError(f"LayerNorm weight/bias must have {D} elements")
+    return x.contiguous(), w, b
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+               eps: float = 1e-6) -> torch.Tensor:
+    """nn.LayerNorm(elementwise_affine=True) over the last dim of a bf16
+    tensor: the DiT block's norm3 before the cross-attention
+    (flashvsr_sm89_ops/integrate.py:171), torch's fp32 arithmetic, one rounding."""
+    x2, w, b = _ln_affine_args(x, weight, bias)
+    out = torch.empty_like(x2)
+    D = x2.shape[-1]
+    _lib.check(_lib.lib().fvsr_layer_norm(x2.data_ptr(), w.data_ptr(), b.data_ptr(),
+                                          out.data_ptr(), x2.numel() // D, D, float(eps), None,
+                                          None, _lib.stream(x2)), "layer_norm")
+    return out
+
+
+def layer_norm_quant(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
+                     eps: float = 1e-6, write_bf16: bool = False):
+    """layer_norm + per-row e4m3 quantisation of its output in one pass.
+    Returns (codes [rows, D] e4m3, row scales [rows, 1] fp32[, bf16 out])."""
+    x2, w, b = _ln_affine_args(x, weight, bias)
+    D = x2.shape[-1]
+    rows = x2.numel() // D
+    q = torch.empty((rows, D), dtype=torch.float8_e4m3fn, device=x2.device)
+    s = torch.empty((rows, 1), dtype=torch.float32, device=x2.device)
+    out = torch.empty_like(x2) if write_bf16 else None
+    _lib.check(_lib.lib().fvsr_layer_norm(x2.data_ptr(), w.data_ptr(), b.data_ptr(),
+                                          _lib.ptr(out), rows, D, float(eps), q.data_ptr(),
+                                          s.data_ptr(), _lib.stream(x2)), "layer_norm_quant")
+    return (q, s, out) if write_bf16 else (q, s)
+
+
+def fused_gate_add_ln_modulate_quant(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor,
+                                     scale: torch.Tensor, shift: torch.Tensor, eps: float = 1e-6,
+                                     write_bf16: bool = False):
+    """x1 = fused_gate_add(x, gate, residual), then fused_ln_modulate_quant(x1,
+    scale, shift), in one pass over the rows: the gated residual that ends a
+    DiT sub-block and the AdaLN that starts the next (integrate.py:151-182).
+    x, residual [B, L, D] bf16 (residual may be a [B*L, D] view); gate,
+    scale, shift [B, 1, D].  Returns (x1, codes [B*L, D] e4m3, row scales
+    [B*L, 1] fp32[, LN-modulated bf16])."""
+    B, L, D = x.shape
+    res = residual.reshape(B, L, D)
+    for t in (x, res, gate, scale, shift):
+        if not t.is_contiguous():
+            raise ValueError("fused_gate_add_ln_modulate_quant: tensors must be contiguous")
+    _lib.require_gpu(x, res, gate, scale, shift)
+    _check_params(x, gate, scale, shift)
+    _lib.require_dtype(res, torch.bfloat16, "residual")
+    x1 = torch.empty_like(x)
+    q = torch.empty((B * L, D), dtype=torch.float8_e4m3fn, device=x.device)
+    s = torch.empty((B * L, 1), dtype=torch.float32, device=x.device)
+    out = torch.empty_like(x) if write_bf16 else None
+    _lib.check(_lib.lib().fvsr_gate_add_ln_modulate(
+        x.data_ptr(), gate.data_ptr(), res.data_ptr(), x1.data_ptr(), scale.data_ptr(),
+        shift.data_ptr(), _lib.ptr(out), B, L, D, float(eps), q.data_ptr(), s.data_ptr(),
+        _lib.stream(x)), "fused_gate_add_ln_modulate_quant")
+    return (x1, q, s, out) if write_bf16 else (x1, q, s)

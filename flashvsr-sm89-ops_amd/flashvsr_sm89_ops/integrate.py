@@ -17,7 +17,12 @@ and before ``pipe.init_cross_kv()``.  In dependency order it
    ``FS89_DRAFT=1`` also computes the draft block mask on the device
    (``lcsa/draft.py``, the bf16 reading of lcsa/reference.py:37-64) in place
    of the DiT's ``generate_draft_block_mask`` (default off: the DiT's own
-   function is the one the reference calls).
+   function is the one the reference calls);
+5. runs the cross-attention's dense attention over the cached prompt K/V on
+   the same HIP attention kernel with every block kept (``FS89_CROSS_ATTN``,
+   default on, shapes it covers: batch 1, head_dim 128, token counts in
+   multiples of 128; others keep the DiT's attention), and with
+   ``FS89_FUSED_ADALN`` the affine ``norm3`` LayerNorm before it.
 
 Re-running ``enable`` on a patched pipeline is safe.  ``FS89_TCDEC_COMPILE``
 (torch.compile of the decoder MemBlocks) is accepted but not applied: it is a
@@ -34,7 +39,9 @@ import torch
 from .compat_bsa import active_backend, ensure_bsa_available
 from .fp8_ffn import convert_ffn_fp8
 from .fp8_linear import convert_linears_fp8
-from .fused_adaln import fused_gate_add, fused_ln_modulate
+from .cross_attn import cross_attention
+from .cross_attn import supported as cross_supported
+from .fused_adaln import fused_gate_add, fused_ln_modulate, layer_norm
 from .fused_rms_rope import fused_rms_rope
 
 
@@ -154,10 +161,24 @@ def _make_cross_attn_forward(dit):
         assert self.cache_k is not None and self.cache_v is not None
         k = self.cache_k
         v = self.cache_v
-        x = self.attn(q, k, v)
+        if _FLAG("FS89_CROSS_ATTN", "1") and cross_supported(q, k, v, self.num_heads):
+            x = cross_attention(q, k, v, self.num_heads)
+        else:
+            x = self.attn(q, k, v)
         return self.o(x)
 
     return torch.no_grad()(forward)
+
+
+def _affine_layer_norm(m):
+    """(weight, bias, eps) when m is an affine nn.LayerNorm over bf16, else None."""
+    m = _unwrap(m)
+    if not isinstance(m, torch.nn.LayerNorm) or not m.elementwise_affine:
+        return None
+    w, b = m.weight, m.bias
+    if w is None or w.dtype != torch.bfloat16 or not w.is_cuda:
+        return None
+    return w, b, m.eps
 
 
 def _make_dit_block_forward(dit):
@@ -183,7 +204,12 @@ def _make_dit_block_forward(dit):
             x = gate_add(x, gate_msa, self_attn_output)
         else:
             x = self.gate(x, gate_msa, self_attn_output)
-        x = x + self.cross_attn(self.norm3(x), context, is_stream=is_stream)
+        ln3 = _affine_layer_norm(self.norm3) if fa is not None else None
+        if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda:
+            normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2])
+        else:
+            normed = self.norm3(x)
+        x = x + self.cross_attn(normed, context, is_stream=is_stream)
         if fa is not None:
             input_x = ln_mod(x, scale_mlp, shift_mlp, eps=_module_eps(self.norm2))
         else:

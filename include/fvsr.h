@@ -127,6 +127,33 @@ int fvsr_ln_modulate(const void* x, const void* scale, const void* shift, void* 
                      int64_t B, int64_t L, int64_t D, float eps, void* codes, float* row_scale,
                      void* stream);
 
+/*
+ * The gated residual of the op before followed by the next AdaLN, in one
+ * pass: x1 = bf16(x + bf16(gate*res)) (fused_gate_add, fused_adaln.py:74-85,
+ * written to x1) then fvsr_ln_modulate of x1 with (scale, shift) into out
+ * and/or the per-row e4m3 codes — the gate_add at the end of the
+ * self-attention (or FFN) and the AdaLN at the start of the FFN (or the next
+ * block's self-attention) of integrate.py:151-182.  x, res, x1 bf16 [B,L,D];
+ * gate, scale, shift bf16 [B,1,D].  Requires D % 8 == 0, D <= 1536 and
+ * 16-byte aligned tensors.
+ */
+int fvsr_gate_add_ln_modulate(const void* x, const void* gate, const void* res, void* x1,
+                              const void* scale, const void* shift, void* out, int64_t B,
+                              int64_t L, int64_t D, float eps, void* codes, float* row_scale,
+                              void* stream);
+
+/*
+ * LayerNorm with affine weight and bias, the DiT block's norm3 before the
+ * cross-attention (x + cross_attn(norm3(x)), integrate.py:171; upstream
+ * nn.LayerNorm, elementwise_affine=True): x, out bf16 [rows, D]; weight, bias
+ * bf16 [D]; y = bf16(w * ((x - mean) * rsqrt(var + eps)) + b) in fp32.  As
+ * in fvsr_ln_modulate, out may be NULL when codes (uint8 [rows, D]) and
+ * row_scale (float [rows]) take the per-row e4m3 quantisation of y for the
+ * FP8 q projection that follows.
+ */
+int fvsr_layer_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
+                    int64_t D, float eps, void* codes, float* row_scale, void* stream);
+
 /* out = bf16(x + bf16(gate*res)), reference fused_gate_add
  * (fused_adaln.py:45-57,74-85): x, res, out bf16 [B,L,D]; gate bf16 [B,1,D]. */
 int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out, int64_t B,

@@ -435,6 +435,55 @@ def dense_masked_attention(q, k, v, keep, sm_scale=None, block: int = 128) -> np
     return out
 
 
+def layer_norm_affine(x: np.ndarray, weight: np.ndarray, bias: np.ndarray,
+                      eps: float = 1e-6) -> np.ndarray:
+    """nn.LayerNorm(elementwise_affine=True) on bf16 values over the last dim,
+    the DiT block's norm3 (integrate.py:171): mean and biased variance, then
+    bf16(w * ((x - mean) / sqrt(var + eps)) + b) with one rounding; computed in
+    float64 (torch computes it in fp32, which differs only where the float64
+    value sits at a bf16 rounding boundary)."""
+    x = np.asarray(x, np.float64)
+    mean = x.mean(-1, keepdims=True)
+    var = ((x - mean) ** 2).mean(-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps) * np.asarray(weight, np.float64) + np.asarray(bias, np.float64)
+    return bf16(y.astype(np.float32))
+
+
+def dense_attention(q, k, v, sm_scale=None) -> np.ndarray:
+    """softmax(q k^T * scale) v per head in float64; q [Lq, H, D], k/v [Lk, H, D]
+    (the cross-attention over the cached prompt K/V, integrate.py:141-143)."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    Lq, H, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    out = np.empty_like(q)
+    for h in range(H):
+        s = q[:, h] @ k[:, h].T * sm_scale
+        s -= s.max(-1, keepdims=True)
+        p = np.exp(s)
+        p /= p.sum(-1, keepdims=True)
+        out[:, h] = p @ v[:, h]
+    return out
+
+
+def cross_attention_block(x, norm3_w, norm3_b, params_q, norm_q_w, cache_k, cache_v, params_o,
+                          heads: int = 12, eps: float = 1e-6, per_token: bool = True):
+    """x + cross_attn(norm3(x)) on [L, dim] bf16 values (integrate.py:132-143,171):
+    LayerNorm(affine) -> FP8 q -> RMSNorm (no RoPE) -> dense attention over the
+    cached K/V [Lk, dim] -> FP8 o -> residual add in bf16."""
+    L, dim = x.shape
+    xin = layer_norm_affine(x, norm3_w, norm3_b, eps)
+    q = linear_fp8(xin, *params_q, per_token=per_token)
+    q = rms_rope(q[None], norm_q_w, eps=eps, rope=False)[0]
+    hd = dim // heads
+    att = bf16(dense_attention(q.reshape(L, heads, hd), np.asarray(cache_k).reshape(-1, heads, hd),
+                               np.asarray(cache_v).reshape(-1, heads, hd)).astype(np.float32))
+    o = linear_fp8(att.reshape(L, dim), *params_o, per_token=per_token)
+    return bf16(np.asarray(x, np.float32) + o)
+
+
 # ----------------------------------------------------------------------------
 # DiT block composition (the C5 unit; integrate.py:151-182 with 47-124)
 # ----------------------------------------------------------------------------
@@ -453,13 +502,16 @@ def ffn_fp8(x: np.ndarray, w1q, w1s, b1, w2q, w2s, b2, per_token: bool = True) -
     return fp8_gemm(hq, hs, w2q, w2s, b2)
 
 
-def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6):
+def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6,
+              cross=None):
     """One DiT block of the C5 stack on [L, dim] bf16 values (batch 1):
     AdaLN -> FP8 q/k/v -> RMSNorm+RoPE(q,k) -> window partition (2,8,8) ->
     block-sparse attention -> reverse -> FP8 o -> gate_add -> AdaLN ->
     FP8 GELU FFN -> gate_add (integrate.py:151-182 without cross-attention).
     ``mod`` is [6, dim] = modulation + t_mod; params holds the quantised
-    weights: q,k,v,o,ffn0,ffn2 as (codes, scale, bias) and norm_q/norm_k."""
+    weights: q,k,v,o,ffn0,ffn2 as (codes, scale, bias) and norm_q/norm_k.
+    ``cross`` (norm3_w, norm3_b, q, o, norm_q, k, v) adds the cross-attention
+    residual after the self-attention one (integrate.py:171)."""
     f, h, w = fhw
     L, dim = x.shape
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = [mod[i][None, None] for i in range(6)]
@@ -476,6 +528,9 @@ def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float =
     att = window_reverse(att, (f, h, w))[0]
     o = linear_fp8(att, *params["o"])
     x = gate_add(x[None], gate_msa, o[None])[0]
+    if cross is not None:
+        x = cross_attention_block(x, cross["norm3_w"], cross["norm3_b"], cross["q"],
+                                  cross["norm_q"], cross["k"], cross["v"], cross["o"], heads, eps)
     xin = ln_modulate(x[None], scale_mlp, shift_mlp, eps)[0]
     y = ffn_fp8(xin, *params["ffn0"], *params["ffn2"])
     return gate_add(x[None], gate_mlp, y[None])[0]

@@ -269,3 +269,34 @@ def test_window_token_map_matches_partition():
     x = np.arange(f * h * w, dtype=np.float32).reshape(1, f, h, w, 1)
     xw = O.window_partition(x).reshape(-1)
     assert np.array_equal(window_token_map(f, h, w).numpy(), xw.astype(np.int32))
+
+
+def test_stock_branch_cross_attention_on_cpu(monkeypatch):
+    """The rebound CrossAttention.forward keeps the DiT's own attention where
+    the HIP kernel does not apply (here: CPU tensors), with the stock RMSNorm
+    when the fused flag is off (integrate.py:132-143)."""
+    import flashvsr_sm89_ops as f
+    from flashvsr_sm89_ops.cross_attn import supported
+    dit = make_fake_dit()
+    monkeypatch.setenv("FS89_FP8", "")
+    monkeypatch.setenv("FS89_FUSED_ROPE", "0")
+    f.enable(FakePipe(), dit_module=dit, verbose=False)
+    ca = dit.CrossAttention()
+    ca.q = torch.nn.Linear(16, 16)
+    ca.o = torch.nn.Linear(16, 16)
+    ca.norm_q = lambda t: t * 3
+    ca.num_heads = 2
+    ca.cache_k, ca.cache_v = torch.randn(1, 7, 16), torch.randn(1, 7, 16)
+    seen = {}
+
+    def attn(q, k, v):
+        seen["args"] = (q, k, v)
+        return q + 1
+    ca.attn = attn
+    x = torch.randn(1, 5, 16)
+    out = ca(x, None)
+    q, k, v = seen["args"]
+    torch.testing.assert_close(q, ca.q(x) * 3)
+    assert k is ca.cache_k and v is ca.cache_v
+    torch.testing.assert_close(out, ca.o(ca.q(x) * 3 + 1))
+    assert not supported(q, k, v, 2)

@@ -400,6 +400,39 @@ def test_draft_mask_bf16_matches_torch_bf16_run(seed, scale, empty_row):
         assert not np.array_equal(k32, _torch_bf16_draft(qb, kb, H, 2, local, 60)[0])
 
 
+@pytest.mark.parametrize("seed,scale", [(12, 1.0), (13, 30.0)])
+def test_layer_norm_affine_vs_torch_bf16(seed, scale):
+    """norm3: torch's own LayerNorm(elementwise_affine=True) on bf16 CPU tensors
+    against the oracle; equal except where the float64 value sits within an
+    fp32 rounding of a bf16 boundary."""
+    rng = np.random.default_rng(seed)
+    x = O.bf16(rng.standard_normal((64, 1536)).astype(np.float32) * scale + 0.5)
+    w = O.bf16((1 + 0.1 * rng.standard_normal(1536)).astype(np.float32))
+    b = O.bf16((0.1 * rng.standard_normal(1536)).astype(np.float32))
+    ref = F.layer_norm(torch.from_numpy(x).bfloat16(), (1536,), torch.from_numpy(w).bfloat16(),
+                       torch.from_numpy(b).bfloat16(), eps=1e-6).float().numpy()
+    got = O.layer_norm_affine(x, w, b, 1e-6)
+    ulp = np.abs(O.bf16_bits(got).astype(np.int32) - O.bf16_bits(ref).astype(np.int32))
+    assert ulp.max() <= 1 and (ulp == 0).mean() > 0.99
+    # without affine parameters it is the LayerNorm inside ln_modulate
+    plain = O.layer_norm_affine(x, np.ones(1536, np.float32), np.zeros(1536, np.float32))
+    ref0 = F.layer_norm(torch.from_numpy(x).bfloat16(), (1536,), eps=1e-6).float().numpy()
+    assert np.abs(O.bf16_bits(plain).astype(np.int32) - O.bf16_bits(ref0).astype(np.int32)).max() <= 1
+
+
+def test_dense_attention_vs_masked_and_sdpa():
+    rng = np.random.default_rng(14)
+    q = rng.standard_normal((256, 2, 64))
+    k = rng.standard_normal((384, 2, 64))
+    v = rng.standard_normal((384, 2, 64))
+    got = O.dense_attention(q, k, v)
+    keep = np.ones((2, 2, 3), bool)
+    assert np.allclose(got, O.dense_masked_attention(q, k, v, keep), atol=1e-12)
+    t = [torch.from_numpy(a).permute(1, 0, 2)[None] for a in (q, k, v)]
+    ref = F.scaled_dot_product_attention(*t)[0].permute(1, 0, 2).numpy()
+    assert np.allclose(got, ref, atol=1e-10)
+
+
 def test_window_partition_roundtrip_and_token_map():
     rng = np.random.default_rng(7)
     x = rng.standard_normal((1, 4, 16, 24, 3)).astype(np.float32)
