@@ -92,7 +92,8 @@ def _modulation(wts: DiTBlockWeights, t_mod: torch.Tensor):
 
 def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor, cs: torch.Tensor,
                       index, tok_map: torch.Tensor, heads: int = 12, eps: float = 1e-6,
-                      hook=None, x8s=None, next_wts: DiTBlockWeights | None = None):
+                      hook=None, x8s=None, next_wts: DiTBlockWeights | None = None,
+                      mods=None, next_mods=None):
     """x [1, L, dim] bf16 (raster order) -> [1, L, dim].  ``index`` is the
     device block index (sel, cnt, maxk) of the attention mask; ``tok_map``
     is window_token_map(f, h, w); ``cs`` the (cos, sin) table [L, 64, 2].
@@ -100,13 +101,16 @@ def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor
     Each gated residual (integrate.py:163-182) is fused with the AdaLN that
     follows it: the self-attention's with the FFN's, the FFN's with the next
     block's (when ``next_wts`` is given; the result is then (y, the next
-    block's input codes), which that block takes as ``x8s``).
+    block's input codes), which that block takes as ``x8s``).  ``mods`` /
+    ``next_mods``, if given, are the six [1, 1, dim] modulation vectors of
+    this / the next block, already added to t_mod.
     ``hook(name)``, if given, is called on the host before each launch group
     and with ``"end"`` after the last (used to place timing events)."""
     mark = hook or (lambda name: None)
     B, L, D = x.shape
     hd = D // heads
-    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = _modulation(wts, t_mod)
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = (
+        mods if mods is not None else _modulation(wts, t_mod))
 
     if x8s is None:
         mark("ln_modulate_quant")
@@ -151,7 +155,7 @@ def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor
     mark("gemm_ffn2")
     yf = fp8_gemm(h8, hs, *wts.ffn2)
     if next_wts is not None:
-        n_shift, n_scale = _modulation(next_wts, t_mod)[:2]
+        n_shift, n_scale = (next_mods if next_mods is not None else _modulation(next_wts, t_mod))[:2]
         mark("gate_add_ln_modulate_quant")
         x2, x8n, xsn = fused_gate_add_ln_modulate_quant(x1, gate_mlp, yf, n_scale, n_shift, eps)
         mark("end")
@@ -172,14 +176,21 @@ class DiTStack:
         self.heads = heads
         self.weights = [DiTBlockWeights(dim, ffn_dim, device, g, cross_len=cross_len)
                         for _ in range(blocks)]
+        self._mod_stack = None
 
     def __call__(self, x, t_mod, cs, index, tok_map, hook=None):
+        # Every block's modulation + t_mod in one launch: [blocks, 6, dim].
+        if self._mod_stack is None:
+            self._mod_stack = torch.cat([w.modulation for w in self.weights]).contiguous()
+        mod = self._mod_stack + t_mod
+        mods = [[mod[i:i + 1, j:j + 1] for j in range(6)] for i in range(len(self.weights))]
         x8s = None
         n = len(self.weights)
         for i, w in enumerate(self.weights):
             nxt = self.weights[i + 1] if i + 1 < n else None
             r = dit_block_forward(x, w, t_mod, cs, index, tok_map, self.heads, hook=hook,
-                                  x8s=x8s, next_wts=nxt)
+                                  x8s=x8s, next_wts=nxt, mods=mods[i],
+                                  next_mods=mods[i + 1] if nxt is not None else None)
             if nxt is None:
                 x = r
             else:
