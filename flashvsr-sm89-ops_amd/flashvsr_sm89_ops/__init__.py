@@ -15,7 +15,8 @@ from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qk  # noqa: E402
 from .fused_adaln import (fused_ln_modulate, fused_gate_add, fused_ln_modulate_quant,  # noqa: E402
                           layer_norm, layer_norm_quant)
 from .fp8_quant import quantize_fp8, quantize_weight_fp8, FP8_MAX  # noqa: E402
-from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm  # noqa: E402
+from .fp8_linear import (FP8Linear, convert_linears_fp8, fp8_gemm,  # noqa: E402
+                         load_fp8_weights, save_fp8_weights)
 from .fp8_ffn import FP8FFN, convert_ffn_fp8, fused_gelu_quant_fp8  # noqa: E402
 from .integrate import enable  # noqa: E402
 from .lcsa import block_sparse_attention, build_csr, draft_block_mask  # noqa: E402
@@ -37,6 +38,8 @@ __all__ = [
     "FP8_MAX",
     "FP8Linear",
     "convert_linears_fp8",
+    "save_fp8_weights",
+    "load_fp8_weights",
     "fp8_gemm",
     "FP8FFN",
     "convert_ffn_fp8",

@@ -60,20 +60,43 @@ def fp8_gemm(x8: torch.Tensor, s: torch.Tensor, w8: torch.Tensor, w_scale: torch
 class FP8Linear(nn.Module):
     """Drop-in for the reference FP8Linear (fp8_linear.py:16-42)."""
 
-    def __init__(self, linear: nn.Linear, per_channel: bool = False, per_token: bool = False):
+    def __init__(self, linear: nn.Linear | None, per_channel: bool = False,
+                 per_token: bool = False):
         super().__init__()
-        w = linear.weight.detach()
-        q, s = quantize_weight_fp8(w.to(torch.bfloat16), per_channel=per_channel)
-        self.w_scale = s
-        self.weight = nn.Parameter(q, requires_grad=False)
-        if linear.bias is not None:
-            self.bias = nn.Parameter(linear.bias.detach().clone(), requires_grad=False)
-        else:
-            self.bias = None
         self.per_channel = per_channel
         self.per_token = per_token
-        self.in_features = w.shape[1]
-        self.out_features = w.shape[0]
+        if linear is None:  # filled by from_quantized
+            return
+        w = linear.weight.detach()
+        q, s = quantize_weight_fp8(w.to(torch.bfloat16), per_channel=per_channel)
+        bias = linear.bias.detach().clone() if linear.bias is not None else None
+        self._set(q, s, bias)
+
+    def _set(self, weight8: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None):
+        self.w_scale = w_scale
+        self.weight = nn.Parameter(weight8, requires_grad=False)
+        self.bias = nn.Parameter(bias, requires_grad=False) if bias is not None else None
+        self.out_features, self.in_features = weight8.shape
+
+    @classmethod
+    def from_quantized(cls, weight8: torch.Tensor, w_scale: torch.Tensor,
+                       bias: torch.Tensor | None = None, per_token: bool = False) -> "FP8Linear":
+        """An FP8Linear from stored codes (float8_e4m3fn, or their uint8 bit
+        patterns) [N, K] and scales (0-dim / [1] per tensor, [N] per channel),
+        without quantising again."""
+        if weight8.dtype == torch.uint8:
+            weight8 = weight8.view(torch.float8_e4m3fn)
+        if weight8.dtype != torch.float8_e4m3fn or weight8.dim() != 2:
+            raise ValueError("from_quantized: weight must be e4m3 codes [N, K]")
+        N = weight8.shape[0]
+        w_scale = w_scale.float()
+        if w_scale.numel() not in (1, N):
+            raise ValueError(f"from_quantized: {w_scale.numel()} scales for {N} output channels")
+        if w_scale.numel() == 1:
+            w_scale = w_scale.reshape(())  # the reference keeps a 0-dim per-tensor scale
+        m = cls(None, per_channel=w_scale.numel() == N and N != 1, per_token=per_token)
+        m._set(weight8.contiguous(), w_scale, bias)
+        return m
 
     def _mm(self, x8, s, out=None):
         return fp8_gemm(x8, s, self.weight, self.w_scale, self.bias, out=out)
@@ -93,10 +116,12 @@ class FP8Linear(nn.Module):
 
 
 def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_channel: bool = False,
-                        per_token: bool = False) -> int:
+                        per_token: bool = False, stored: dict | None = None) -> int:
     """Convert DiT-block Linears whose module names match `parts`
     ("ffn" / "self" / "cross"); returns the number converted
-    (fp8_linear.py:45-67).  Idempotent: FP8Linear is not an nn.Linear."""
+    (fp8_linear.py:45-67).  Idempotent: FP8Linear is not an nn.Linear.
+    ``stored`` (from load_fp8_weights) supplies saved codes and scales by
+    module name; those modules are not quantised again."""
     allowed = []
     if "self" in parts:
         allowed.append(r"^blocks\.\d+\.self_attn\.[qkvo]$")
@@ -111,6 +136,60 @@ def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_ch
             continue
         parent_name, _, leaf = name.rpartition(".")
         parent = model.get_submodule(parent_name) if parent_name else model
-        setattr(parent, leaf, FP8Linear(mod, per_channel=per_channel, per_token=per_token))
+        if stored is not None and name in stored:
+            w8, ws, b = stored[name]
+            if tuple(w8.shape) != tuple(mod.weight.shape):
+                raise ValueError(f"stored FP8 weight for {name} has shape {tuple(w8.shape)}, "
+                                 f"the module {tuple(mod.weight.shape)}")
+            if (ws.numel() == w8.shape[0] and w8.shape[0] != 1) != per_channel:
+                raise ValueError(f"stored FP8 weight for {name} has the other scale granularity")
+            dev = mod.weight.device
+            new = FP8Linear.from_quantized(w8.to(dev), ws.to(dev),
+                                           b.to(dev) if b is not None else None, per_token)
+        else:
+            new = FP8Linear(mod, per_channel=per_channel, per_token=per_token)
+        setattr(parent, leaf, new)
         n += 1
     return n
+
+
+FP8_WEIGHTS_FORMAT = "flashvsr-fp8-weights/1"
+
+
+def save_fp8_weights(model: nn.Module, path: str) -> int:
+    """Persist every FP8Linear of ``model`` (codes as uint8 bit patterns, fp32
+    scales, bf16 biases) to a safetensors file; returns the number saved.
+    Reloading gives bit-identical modules without quantising again."""
+    from safetensors.torch import save_file
+    tensors = {}
+    n = 0
+    for name, mod in model.named_modules():
+        if not isinstance(mod, FP8Linear):
+            continue
+        tensors[f"{name}.weight"] = mod.weight.detach().view(torch.uint8).contiguous().cpu()
+        tensors[f"{name}.w_scale"] = mod.w_scale.detach().float().reshape(-1).contiguous().cpu()
+        if mod.bias is not None:
+            tensors[f"{name}.bias"] = mod.bias.detach().contiguous().cpu()
+        n += 1
+    save_file(tensors, path, metadata={"format": FP8_WEIGHTS_FORMAT})
+    return n
+
+
+def load_fp8_weights(path: str) -> dict:
+    """{module name: (codes uint8 [N, K], scales fp32, bias or None)} from a
+    file written by save_fp8_weights (CPU tensors; nothing is executed from
+    the file)."""
+    from safetensors import safe_open
+    out = {}
+    with safe_open(path, framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("format") != FP8_WEIGHTS_FORMAT:
+            raise ValueError(f"{path}: not a {FP8_WEIGHTS_FORMAT} file")
+        keys = set(f.keys())
+        for k in sorted(keys):
+            if not k.endswith(".weight"):
+                continue
+            name = k[:-len(".weight")]
+            b = f.get_tensor(f"{name}.bias") if f"{name}.bias" in keys else None
+            out[name] = (f.get_tensor(k), f.get_tensor(f"{name}.w_scale"), b)
+    return out

@@ -38,7 +38,7 @@ import torch
 
 from .compat_bsa import active_backend, ensure_bsa_available
 from .fp8_ffn import convert_ffn_fp8
-from .fp8_linear import convert_linears_fp8
+from .fp8_linear import convert_linears_fp8, load_fp8_weights, save_fp8_weights
 from .cross_attn import cross_attention
 from .cross_attn import supported as cross_supported
 from .fused_adaln import fused_gate_add, fused_ln_modulate, layer_norm
@@ -268,9 +268,12 @@ def _patch_dit(dit, fused_rope, fused_adaln):
 
 
 def enable(pipe, dit_module=None, parts=None, compile_memblocks=None, verbose=True,
-           scale_granularity=None):
+           scale_granularity=None, fp8_weights=None):
     """Apply the operator pack to a FlashVSRTinyPipeline; returns a dict of
-    what was enabled (same keys as the reference)."""
+    what was enabled (same keys as the reference).  ``fp8_weights`` (or
+    ``FS89_FP8_WEIGHTS``) names a file of quantised weights: loaded instead of
+    quantising when it exists, written after the conversion when it does not
+    (then ``applied["fp8_weights"]`` says which)."""
     if parts is None:
         parts = [p for p in os.environ.get("FS89_FP8", "ffn,self,cross").split(",") if p]
     if compile_memblocks is None:
@@ -300,10 +303,19 @@ def enable(pipe, dit_module=None, parts=None, compile_memblocks=None, verbose=Tr
                       "operator pack (decoder-side torch.compile is outside the pack).")
         applied["tcdec_compiled_memblocks"] = 0
 
+    if fp8_weights is None:
+        fp8_weights = os.environ.get("FS89_FP8_WEIGHTS") or None
     if parts:
+        stored = None
+        if fp8_weights and os.path.exists(fp8_weights):
+            stored = load_fp8_weights(fp8_weights)
+            applied["fp8_weights"] = "loaded"
         n = convert_linears_fp8(pipe.denoising_model(), parts=parts, per_channel=row,
-                                per_token=row)
+                                per_token=row, stored=stored)
         applied["fp8_linears"] = n
+        if fp8_weights and stored is None and n:
+            save_fp8_weights(pipe.denoising_model(), fp8_weights)
+            applied["fp8_weights"] = "saved"
         if "ffn" in parts and _FLAG("FS89_FP8_FFNFUSED", "1"):
             applied["fp8_ffn_blocks"] = convert_ffn_fp8(pipe.denoising_model())
 

@@ -201,3 +201,36 @@ def test_dit_stack_two_blocks_vs_oracle():
         mod = (wts.modulation.cpu().float() + t_mod.float()).to(torch.bfloat16).float().numpy()[0]
         ref = O.dit_block(ref, mod, params, (f, h, w), keep, cos, sin, heads)
     _close(host_f(y)[0], ref)
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_fp8_weights_persist_bit_identical(tmp_path, per_channel):
+    """Weights quantised on the device, saved, and loaded into a fresh model
+    give the same codes, scales and forward outputs bit for bit."""
+    import copy
+    from flashvsr_sm89_ops.fp8_linear import (convert_linears_fp8, load_fp8_weights,
+                                              save_fp8_weights)
+    g = torch.Generator().manual_seed(11)
+    model = torch.nn.Module()
+    model.blocks = torch.nn.ModuleList([torch.nn.Module()])
+    model.blocks[0].cross_attn = torch.nn.Module()
+    for n in "qo":
+        lin = torch.nn.Linear(1536, 1536)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(1536, 1536, generator=g) * 0.02)
+            lin.bias.copy_(torch.randn(1536, generator=g) * 0.1)
+        setattr(model.blocks[0].cross_attn, n, lin)
+    model = model.to(DEV).to(torch.bfloat16)
+    fresh = copy.deepcopy(model)
+    assert convert_linears_fp8(model, parts=("cross",), per_channel=per_channel,
+                               per_token=per_channel) == 2
+    path = str(tmp_path / "w.safetensors")
+    save_fp8_weights(model, path)
+    assert convert_linears_fp8(fresh, parts=("cross",), per_channel=per_channel,
+                               per_token=per_channel, stored=load_fp8_weights(path)) == 2
+    x = torch.randn(1, 256, 1536, generator=g).to(torch.bfloat16).to(DEV)
+    for n in "qo":
+        a, b = getattr(model.blocks[0].cross_attn, n), getattr(fresh.blocks[0].cross_attn, n)
+        assert torch.equal(a.weight.view(torch.uint8), b.weight.view(torch.uint8))
+        assert torch.equal(a.w_scale, b.w_scale) and torch.equal(a.bias, b.bias)
+        assert torch.equal(a(x), b(x))

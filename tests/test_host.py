@@ -300,3 +300,95 @@ def test_stock_branch_cross_attention_on_cpu(monkeypatch):
     assert k is ca.cache_k and v is ca.cache_v
     torch.testing.assert_close(out, ca.o(ca.q(x) * 3 + 1))
     assert not supported(q, k, v, 2)
+
+
+def _dit_like(dim=16, ffn=32):
+    m = torch.nn.Module()
+    m.blocks = torch.nn.ModuleList()
+    for _ in range(2):
+        b = torch.nn.Module()
+        b.self_attn = torch.nn.Module()
+        for n in "qkvo":
+            setattr(b.self_attn, n, torch.nn.Linear(dim, dim))
+        b.ffn = torch.nn.Sequential(torch.nn.Linear(dim, ffn), torch.nn.GELU(),
+                                    torch.nn.Linear(ffn, dim, bias=False))
+        m.blocks.append(b)
+    return m
+
+
+def _stored_for(model, per_channel, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for name, mod in model.named_modules():
+        if isinstance(mod, torch.nn.Linear):
+            N, K = mod.weight.shape
+            codes = torch.randint(0, 256, (N, K), generator=g, dtype=torch.int64).to(torch.uint8)
+            scales = torch.rand(N if per_channel else 1, generator=g) + 0.01
+            bias = mod.bias.detach().to(torch.bfloat16) if mod.bias is not None else None
+            out[name] = (codes, scales, bias)
+    return out
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_fp8_weights_save_load_roundtrip(tmp_path, per_channel):
+    """Stored codes and scales come back bit for bit; conversion from them
+    quantises nothing (so it runs here, without the GPU library)."""
+    from flashvsr_sm89_ops.fp8_linear import (FP8Linear, convert_linears_fp8, load_fp8_weights,
+                                              save_fp8_weights)
+    model = _dit_like()
+    stored = _stored_for(model, per_channel)
+    n = convert_linears_fp8(model, parts=("self", "ffn"), per_channel=per_channel, stored=stored)
+    assert n == 12
+    for name, (codes, scales, bias) in stored.items():
+        mod = model.get_submodule(name)
+        assert isinstance(mod, FP8Linear) and mod.weight.dtype == torch.float8_e4m3fn
+        assert torch.equal(mod.weight.view(torch.uint8), codes)
+        assert torch.equal(mod.w_scale.reshape(-1), scales)
+        assert mod.per_channel == per_channel and (mod.w_scale.dim() == 0) != per_channel
+    path = str(tmp_path / "w.safetensors")
+    assert save_fp8_weights(model, path) == 12
+    back = load_fp8_weights(path)
+    assert set(back) == set(stored)
+    for name, (codes, scales, bias) in stored.items():
+        c2, s2, b2 = back[name]
+        assert torch.equal(c2, codes) and torch.equal(s2, scales)
+        assert (b2 is None) == (bias is None) and (bias is None or torch.equal(b2, bias))
+    fresh = _dit_like()
+    assert convert_linears_fp8(fresh, parts=("self", "ffn"), per_channel=per_channel,
+                               stored=back) == 12
+    for name in stored:
+        assert torch.equal(fresh.get_submodule(name).weight.view(torch.uint8),
+                           model.get_submodule(name).weight.view(torch.uint8))
+
+
+def test_fp8_weights_rejects_mismatch(tmp_path):
+    from flashvsr_sm89_ops.fp8_linear import convert_linears_fp8, load_fp8_weights
+    model = _dit_like()
+    stored = _stored_for(model, per_channel=True)
+    with pytest.raises(ValueError, match="granularity"):
+        convert_linears_fp8(_dit_like(), parts=("self",), per_channel=False, stored=stored)
+    stored["blocks.0.self_attn.q"] = (torch.zeros(3, 16, dtype=torch.uint8), torch.ones(3), None)
+    with pytest.raises(ValueError, match="shape"):
+        convert_linears_fp8(_dit_like(), parts=("self",), per_channel=True, stored=stored)
+    from safetensors.torch import save_file
+    other = str(tmp_path / "other.safetensors")
+    save_file({"x": torch.zeros(2)}, other)
+    with pytest.raises(ValueError, match="not a"):
+        load_fp8_weights(other)
+
+
+def test_enable_loads_stored_fp8_weights(tmp_path, monkeypatch):
+    import flashvsr_sm89_ops as f
+    from flashvsr_sm89_ops.fp8_linear import convert_linears_fp8, save_fp8_weights
+    src = _dit_like()
+    convert_linears_fp8(src, parts=("self", "ffn"), stored=_stored_for(src, per_channel=False))
+    path = str(tmp_path / "w.safetensors")
+    save_fp8_weights(src, path)
+    pipe = FakePipe()
+    pipe.model = _dit_like()
+    monkeypatch.setenv("FS89_FP8", "self")
+    monkeypatch.setenv("FS89_FP8_WEIGHTS", path)
+    applied = f.enable(pipe, dit_module=make_fake_dit(), verbose=False)
+    assert applied["fp8_weights"] == "loaded" and applied["fp8_linears"] == 8
+    assert torch.equal(pipe.model.blocks[1].self_attn.o.weight.view(torch.uint8),
+                       src.blocks[1].self_attn.o.weight.view(torch.uint8))
