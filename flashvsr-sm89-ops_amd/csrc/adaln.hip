@@ -227,10 +227,7 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
       for (int j = 0; j < VPL; ++j) {
         const int64_t c = lane + 64 * j;
         if (c < nchunk && l0 + r < L) {
-          u32x2_t q;
-          q[0] = e4m3x4_div(bf_lo(o[j][0]), bf_hi(o[j][0]), bf_lo(o[j][1]), bf_hi(o[j][1]), qs, qr);
-          q[1] = e4m3x4_div(bf_lo(o[j][2]), bf_hi(o[j][2]), bf_lo(o[j][3]), bf_hi(o[j][3]), qs, qr);
-          *(u32x2_t*)(codes + row[r] * D + c * 8) = q;
+          *(u32x2_t*)(codes + row[r] * D + c * 8) = chunk_codes_fma(o[j], qr, fminf(qs, 3.40282347e38f));
         }
       }
       if (lane == 0 && l0 + r < L) row_scale[row[r]] = amax / 448.0f;
@@ -358,10 +355,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_vec(
       for (int j = 0; j < VPL; ++j) {
         const int64_t c = lane + 64 * j;
         if (c < nchunk && r0 + r < rows) {
-          u32x2_t q;
-          q[0] = e4m3x4_div(bf_lo(o[j][0]), bf_hi(o[j][0]), bf_lo(o[j][1]), bf_hi(o[j][1]), qs, qr);
-          q[1] = e4m3x4_div(bf_lo(o[j][2]), bf_hi(o[j][2]), bf_lo(o[j][3]), bf_hi(o[j][3]), qs, qr);
-          *(u32x2_t*)(codes + row[r] * D + c * 8) = q;
+          *(u32x2_t*)(codes + row[r] * D + c * 8) = chunk_codes_fma(o[j], qr, fminf(qs, 3.40282347e38f));
         }
       }
       if (lane == 0 && r0 + r < rows) row_scale[row[r]] = amax / 448.0f;

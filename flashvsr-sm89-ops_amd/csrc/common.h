@@ -147,25 +147,46 @@ FVSR_DEV float gelu_tanh_bf16(float x) {
   return round_bf16((0.5f * x) * (1.0f + t));
 }
 
-// e4m3 codes of clamp(v_i / s, +-448) for four values, where v_i / s is the
-// IEEE fp32 division the quantisation contract prescribes.  With r = 1/s
-// (IEEE), y = fl(v * r) lies within 1.5 * 2^-23 (relative) of fl(v / s), so
-// fl(v / s) lies between y * (1 - 2^-21) and y * (1 + 2^-21) (each rounded).
-// When the e4m3 roundings (monotone) of both ends agree, that is the code;
-// otherwise a rounding boundary lies inside the bracket and the division
-// itself decides (rare; taken per wave only when some lane needs it).
-// Precondition: |v_i| <= 448 * s, as for s = max(amax, 1e-12) / 448 over
-// values bounded by amax; then both ends stay below 449 and convert without
-// a clamp (conversions below 464 round to at most 448).
-FVSR_DEV uint32_t e4m3x4_div(float v0, float v1, float v2, float v3, float s, float r) {
-  const float kLo = 0.99999952316284180f, kHi = 1.00000047683715820f;  // 1 -+ 2^-21
-  const float y0 = v0 * r, y1 = v1 * r, y2 = v2 * r, y3 = v3 * r;
-  const uint32_t lo = pack_e4m3x4(y0 * kLo, y1 * kLo, y2 * kLo, y3 * kLo);
-  const uint32_t hi = pack_e4m3x4(y0 * kHi, y1 * kHi, y2 * kHi, y3 * kHi);
-  uint32_t out = lo;
-  if (__builtin_amdgcn_ballot_w64(lo != hi)) {
-    if (lo != hi)
-      out = pack_e4m3x4(clamp448(v0 / s), clamp448(v1 / s), clamp448(v2 / s), clamp448(v3 / s));
+// Four fp32 -> four e4m3fn codes; both halves of the destination are written,
+// so its prior contents (here a's bits, dead after this) do not matter.
+FVSR_DEV uint32_t e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __builtin_bit_cast(int, a), false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+}
+
+// Packed bf16 pair -> the two floats.
+FVSR_DEV float lo_f(uint32_t p) { return __uint_as_float(p << 16); }
+FVSR_DEV float hi_f(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// |v| / s without a division: q0 = |v| * r with r = fl(1/s), the residual
+// e = |v| - q0 * s by one fma, and q0 + e * r by another (Markstein's
+// correction).  Its e4m3 code equals that of the IEEE quotient fl(|v| / s)
+// for every bf16 v and every bf16 amax >= |v|, with s = fl(max(amax, 1e-12) /
+// 448), including amax = inf (sc = min(s, FLT_MAX) keeps the residual finite
+// there): checked exhaustively over all 1.07e9 such pairs
+// (tests/native/fma_quotient_check.c).  The quotient is formed on |v| and the
+// sign put into the code afterwards, so -0 keeps its sign.  |v| <= amax bounds
+// the result by 448 * (1 + 2^-23), which the conversion rounds to 448 without
+// a clamp.
+FVSR_DEV float quot_abs(float v, float r, float sc) {
+  const float a = fabsf(v);
+  const float q0 = a * r;
+  const float e = fmaf(-q0, sc, a);
+  return fmaf(e, r, q0);
+}
+
+// Codes of one chunk (8 packed bf16 values) divided by s (r = fl(1/s),
+// sc = min(s, FLT_MAX)), every value bounded by the amax s was made from.
+// The sign bits of the inputs (bit 7 of bytes 1 and 3 of each dword) are
+// gathered by one byte permute per four values.
+FVSR_DEV u32x2_t chunk_codes_fma(u32x4_t p, float r, float sc) {
+  u32x2_t out;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t p0 = p[2 * h], p1 = p[2 * h + 1];
+    const uint32_t c = e4m3x4(quot_abs(lo_f(p0), r, sc), quot_abs(hi_f(p0), r, sc),
+                              quot_abs(lo_f(p1), r, sc), quot_abs(hi_f(p1), r, sc));
+    out[h] = c | (__builtin_amdgcn_perm(p1, p0, 0x07050301u) & 0x80808080u);
   }
   return out;
 }

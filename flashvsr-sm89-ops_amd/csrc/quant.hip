@@ -7,10 +7,10 @@
 // re-reduces those partials (at most 1024 floats) before quantising, so no
 // atomics and no memset are needed.
 //
-// Bit-exactness: the codes are those of the IEEE division x/s (e4m3x4_div
-// multiplies by 1/s and falls back to the division whenever the product's
-// bracket straddles an e4m3 rounding boundary); the fp32 -> e4m3fn
-// conversion is v_cvt_pk_fp8_f32 after clamping to +-448.
+// Bit-exactness: the codes are those of the IEEE division x/s, formed
+// without dividing (quot_abs in common.h: one product and two fmas, checked
+// exhaustively over bf16 values and scales); the fp32 -> e4m3fn conversion is
+// v_cvt_pk_fp8_f32.
 //
 // GELU of bf16 data (the FFN requantisation) is a lookup: the 65536 bf16
 // results, generated at build time from the operation sequence of
@@ -47,15 +47,9 @@ FVSR_DEV float chunk_absmax(u32x4_t c) {
   return m;
 }
 
-// Codes of 8 bf16 values (x/s each); r = 1/s.
-FVSR_DEV u32x2_t chunk_codes(u32x4_t c, float s, float r) {
-  u32x2_t q;
-  q[0] = e4m3x4_div(bf_lo(c[0]), bf_hi(c[0]), bf_lo(c[1]), bf_hi(c[1]), s, r);
-  q[1] = e4m3x4_div(bf_lo(c[2]), bf_hi(c[2]), bf_lo(c[3]), bf_hi(c[3]), s, r);
-  return q;
-}
-
 FVSR_DEV float qscale(float amax) { return fmaxf(amax, 1e-12f) / 448.0f; }
+// The residual's copy of s, kept finite (s = inf when amax = inf).
+FVSR_DEV float qscale_fin(float s) { return fminf(s, 3.40282347e38f); }
 
 // ---------------------------------------------------------------------------
 // Row mode, register resident: cols % 8 == 0, cols <= 512*VPL, 16-byte rows.
@@ -87,7 +81,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec(
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
     const int64_t c = lane + 64 * j;
-    if (c < nchunk) *(u32x2_t*)(qr + c * 8) = chunk_codes(v[j], s, r);
+    if (c < nchunk) *(u32x2_t*)(qr + c * 8) = chunk_codes_fma(v[j], r, qscale_fin(s));
   }
   if (lane == 0) scale_out[row] = amax / 448.0f;
 }
@@ -102,15 +96,9 @@ __device__ const uint16_t kGeluTable[65536] __attribute__((aligned(16))) = {
 #include "gelu_table.inc"
 };
 
-constexpr int kTabWaves = 8;
-
-FVSR_DEV u32x4_t gelu_lookup(u32x4_t c, const uint16_t* tab) {
-  u32x4_t g;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    g[i] = (uint32_t)tab[c[i] & 0xffffu] | ((uint32_t)tab[c[i] >> 16] << 16);
-  return g;
-}
+// 16 waves (4 per SIMD, at most 128 registers each) share the one table per
+// CU; each holds one row at a time, and the other waves' rows hide its loads.
+constexpr int kTabWaves = 16;
 
 // Load row `row` (chunks past the end of the row repeat its last chunk).
 template <int VPL>
@@ -124,23 +112,43 @@ FVSR_DEV void load_row(u32x4_t (&v)[VPL], const uint16_t* x, int64_t row, int64_
   }
 }
 
+// max(m, |a|, |b|) in one v_max3_f32.  The table holds quiet NaNs only (the
+// GELU of a NaN input), which v_max3_f32 passes over as fmaxf does, and the
+// operands need no canonicalising maximum first.
+FVSR_DEV float max3_abs(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+
+// Row `row` is in v (bf16); its GELU values replace it in place (packed
+// bf16), then the codes are written from there.
 template <int VPL>
 FVSR_DEV void gelu_quant_row(u32x4_t (&v)[VPL], const uint16_t* tab, int64_t row, int64_t cols,
                              int nchunk, uint8_t* codes, float* scale_out) {
   float m = 0.0f;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    v[j] = gelu_lookup(v[j], tab);
-    m = fmaxf(m, chunk_absmax(v[j]));  // a repeated chunk changes no maximum
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[j][i] = (uint32_t)tab[v[j][i] & 0xffffu] | ((uint32_t)tab[v[j][i] >> 16] << 16);
+      m = max3_abs(m, lo_f(v[j][i]), hi_f(v[j][i]));
+    }
   }
-  const float amax = wave_max_abs(m);
-  const float s = qscale(amax), r = 1.0f / s;
+  const float amax = wave_max_abs(m);  // a repeated chunk changes no maximum
+  const float s = qscale(amax), r = 1.0f / s, sc = qscale_fin(s);
   const int lane = lane_here();
   uint8_t* qr = codes + row * cols;
 #pragma unroll
   for (int j = 0; j < VPL; ++j) {
-    const int c = lane + 64 * j;
-    if (c < nchunk) *(u32x2_t*)(qr + (uint32_t)c * 8u) = chunk_codes(v[j], s, r);
+    // Opaque copy: the floats of the maximum pass are not kept for this one
+    // (that would hold 8 registers per chunk instead of 4).
+    asm volatile("" : "+v"(v[j]));
+    const u32x2_t q = chunk_codes_fma(v[j], r, sc);
+    // Past the row's end the chunk is a copy of its last one (load_row), so
+    // its codes go to that chunk's place: same bytes, and no branch.
+    const int c = min(lane + 64 * j, nchunk - 1);
+    *(u32x2_t*)(qr + (uint32_t)c * 8u) = q;
   }
   if (lane == 0) scale_out[row] = amax / 448.0f;
 }
@@ -157,21 +165,11 @@ __global__ __launch_bounds__(kTabWaves * 64) void quant_rows_gelu_table(
   const int64_t stride = (int64_t)gridDim.x * kTabWaves;
   int64_t row = (int64_t)blockIdx.x * kTabWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  u32x4_t va[VPL], vb[VPL];
-  load_row(va, x, row, ld, nchunk);
-  for (;;) {
-    int64_t next = row + stride;
-    load_row(vb, x, next < rows ? next : rows - 1, ld, nchunk);
-    gelu_quant_row(va, tab, row, cols, nchunk, codes, scale_out);
-    if (next >= rows) break;
-    row = next;
-    next = row + stride;
-    load_row(va, x, next < rows ? next : rows - 1, ld, nchunk);
-    gelu_quant_row(vb, tab, row, cols, nchunk, codes, scale_out);
-    if (next >= rows) break;
-    row = next;
+  u32x4_t v[VPL];
+  for (; row < rows; row += stride) {
+    load_row(v, x, row, ld, nchunk);
+    gelu_quant_row<VPL>(v, tab, row, cols, nchunk, codes, scale_out);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // the last prefetch (a repeated row) drains before exit
 }
 
 // Row mode, any shape: two passes over the row (the second hits L2).
@@ -272,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
       for (int64_t c = lane; c < (cols >> 3); c += 64) {
         u32x4_t v = *(const u32x4_t*)(xr + c * 8);
         if (GELU) v = gelu_chunk(v);
-        *(u32x2_t*)(qr + c * 8) = chunk_codes(v, s, r);
+        *(u32x2_t*)(qr + c * 8) = chunk_codes_fma(v, r, qscale_fin(s));
       }
     } else {
       for (int64_t c = lane; c < cols; c += 64) {
@@ -383,8 +381,8 @@ int launch_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8
   if (GELU && vec && vpl <= 18) {
     const int64_t want = (rows + kTabWaves - 1) / kTabWaves;
     const int64_t g = want < cu_count() ? want : cu_count();
-    hipLaunchKernelGGL((quant_rows_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0, st,
-                       x, rows, cols, ld, q, s);
+    hipLaunchKernelGGL((quant_rows_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0,
+                       st, x, rows, cols, ld, q, s);
   } else if (vec && vpl <= 3) {
     hipLaunchKernelGGL((quant_rows_vec<3, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
   } else if (vec && vpl <= 6) {

@@ -171,6 +171,18 @@ def test_gelu_quant_bitexact(ops, shape, per_token):
     assert np.array_equal(host_f(s).reshape(-1), rs)
 
 
+@pytest.mark.parametrize("shape", [(4133, 8960), (4133, 1024)])
+def test_gelu_quant_rows_persistent(ops, shape):
+    """More rows than the persistent table kernel has waves (256 workgroups of
+    8 on MI355X), so each wave loops over several rows and prefetches the next
+    one; about one row in ten takes the division fallback."""
+    h = rnd_bits(shape, seed=7 + shape[1], scale=2.0)
+    q, s = ops.fused_gelu_quant_fp8(dev_bf16(h), per_token=True)
+    rq, rs = O.quantize_fp8(h, per_row=True, gelu=True)
+    assert np.array_equal(host_f(s).reshape(-1), rs)
+    assert np.array_equal(host_codes(q), rq)
+
+
 @pytest.mark.parametrize("shape", [(1536, 1536), (96, 256), (8960, 1536), (7, 100)])
 @pytest.mark.parametrize("per_channel", [True, False])
 def test_weight_quant_bitexact(ops, shape, per_channel):
