@@ -95,6 +95,44 @@ __global__ __launch_bounds__(kThreads) void rms_rope_qk_vec(
                           (isk ? ok : oq) + row * ld_out, D, head_dim, eps, threadIdx.x & 63);
 }
 
+// q (in place or to out_q, same rows), k and v to rows kv_rows[r] of out_k and
+// out_v (the window-ordered K/V buffer of the attention): blockIdx.y picks the
+// tensor; v is a plain row copy.  Rows whose target is outside [0, kv_cap)
+// are not written.
+template <int VPL>
+__global__ __launch_bounds__(kThreads) void rms_rope_qkv_rows_vec(
+    const uint16_t* q, const uint16_t* k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ wq, const uint16_t* __restrict__ wk,
+    const float* __restrict__ cs, uint16_t* oq, uint16_t* __restrict__ ok,
+    uint16_t* __restrict__ ov, const int32_t* __restrict__ kv_rows, int64_t kv_cap,
+    int64_t rows, int64_t L, int64_t D, int64_t head_dim, float eps, int64_t ld_in,
+    int64_t ld_out, int64_t ld_kv) {
+  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  if (blockIdx.y == 0) {
+    rms_rope_row<VPL, true>(q + row * ld_in, wq, cs + (row % L) * head_dim, oq + row * ld_out, D,
+                            head_dim, eps, lane);
+    return;
+  }
+  const int64_t dst = kv_rows[row];
+  if (dst < 0 || dst >= kv_cap) return;
+  if (blockIdx.y == 1) {
+    rms_rope_row<VPL, true>(k + row * ld_in, wk, cs + (row % L) * head_dim, ok + dst * ld_kv, D,
+                            head_dim, eps, lane);
+    return;
+  }
+  const int64_t nchunk = D >> 3;
+  const uint16_t* src = v + row * ld_in;
+  uint16_t* out = ov + dst * ld_kv;
+  u32x4_t t[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) t[j] = *(const u32x4_t*)(src + clamp_chunk(lane + 64 * j, nchunk) * 8);
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+    if (lane + 64 * j < nchunk) *(u32x4_t*)(out + (lane + 64 * j) * 8) = t[j];
+}
+
 // Any shape: scalar loads, partner element read directly.
 __global__ __launch_bounds__(kThreads) void rms_rope_generic(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ cs,
@@ -173,5 +211,31 @@ extern "C" int fvsr_rms_rope_qk(const void* q, const void* k, const void* wq, co
                      dim3(kThreads), 0, st, (const uint16_t*)q, (const uint16_t*)k,
                      (const uint16_t*)wq, (const uint16_t*)wk, cs, (uint16_t*)out_q,
                      (uint16_t*)out_k, rows, L, D, head_dim, eps, ld_in, ld_out);
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_rms_rope_qkv_rows(const void* q, const void* k, const void* v, const void* wq,
+                                      const void* wk, const float* cs, void* out_q, void* out_k,
+                                      void* out_v, const int32_t* kv_rows, int64_t kv_cap,
+                                      int64_t B, int64_t L, int64_t D, int64_t head_dim,
+                                      float eps, int64_t ld_in, int64_t ld_out, int64_t ld_kv,
+                                      void* stream) {
+  if (B < 0 || L < 0 || D <= 0 || head_dim <= 0 || head_dim % 8 || D % head_dim) return FVSR_EINVAL;
+  if (ld_in < D || ld_out < D || ld_kv < D || kv_cap < 0) return FVSR_EINVAL;
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!q || !k || !v || !wq || !wk || !cs || !out_q || !out_k || !out_v || !kv_rows)
+    return FVSR_EINVAL;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && ld_in % 8 == 0 && ld_out % 8 == 0 &&
+                   ld_kv % 8 == 0 && aligned16(q) && aligned16(k) && aligned16(v) &&
+                   aligned16(wq) && aligned16(wk) && aligned16(cs) && aligned16(out_q) &&
+                   aligned16(out_k) && aligned16(out_v);
+  if (!vec) return FVSR_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL((rms_rope_qkv_rows_vec<3>), dim3((unsigned)((rows + kWaves - 1) / kWaves), 3),
+                     dim3(kThreads), 0, st, (const uint16_t*)q, (const uint16_t*)k,
+                     (const uint16_t*)v, (const uint16_t*)wq, (const uint16_t*)wk, cs,
+                     (uint16_t*)out_q, (uint16_t*)out_k, (uint16_t*)out_v, kv_rows, kv_cap, rows,
+                     L, D, head_dim, eps, ld_in, ld_out, ld_kv);
   return fvsr_launch_status();
 }

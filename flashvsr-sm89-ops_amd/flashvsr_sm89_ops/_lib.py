@@ -49,6 +49,8 @@ _SIGS = {
     "fvsr_rms_rope": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P], _I),
     "fvsr_rms_rope_qk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I64, _I64,
                           _P], _I),
+    "fvsr_rms_rope_qkv_rows": ([_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64,
+                                _I64, _F, _I64, _I64, _I64, _P], _I),
     "fvsr_block_index": ([_P, _I64, _I64, _I64, _P, _P, _P], _I),
     "fvsr_draft_workspace_floats": ([_I64, _I64, _I64, _I64], _I64),
     "fvsr_draft_block_mask": ([_P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P,

@@ -104,3 +104,37 @@ def fused_rms_rope_qk(q: torch.Tensor, k: torch.Tensor, weight_q: torch.Tensor,
                                            q.stride(1), oq.stride(1), _lib.stream(q)),
                "fused_rms_rope_qk")
     return oq, ok
+
+
+def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                            weight_q: torch.Tensor, weight_k: torch.Tensor, freqs_cis,
+                            out_k: torch.Tensor, out_v: torch.Tensor, kv_rows: torch.Tensor,
+                            eps: float = 1e-6, head_dim: int = 128) -> torch.Tensor:
+    """The self-attention's RMSNorm + RoPE of q and k (integrate.py:59-62)
+    with k and v written straight into a window-ordered K/V buffer
+    (integrate.py:70-83 without the partition and cat copies).  q, k, v:
+    [B, L, D] bf16 with contiguous rows; q is rotated in place and returned;
+    row r of k and v goes to row ``kv_rows[r]`` of ``out_k`` / ``out_v``
+    ([rows, D] bf16, contiguous)."""
+    _lib.require_gpu(q, k, v, weight_q, weight_k, out_k, out_v, kv_rows)
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out_k, "out_k"), (out_v, "out_v")):
+        _lib.require_dtype(t, torch.bfloat16, n)
+    _lib.require_dtype(kv_rows, torch.int32, "kv_rows")
+    B, L, D = q.shape
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("fused_rms_rope_qkv_rows: q, k, v shapes differ")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("fused_rms_rope_qkv_rows: q, k, v must be contiguous")
+    if out_k.shape != out_v.shape or out_k.dim() != 2 or out_k.shape[1] != D or \
+            not (out_k.is_contiguous() and out_v.is_contiguous()):
+        raise ValueError("fused_rms_rope_qkv_rows: out_k/out_v must be contiguous [rows, D]")
+    if kv_rows.numel() != B * L or not kv_rows.is_contiguous():
+        raise ValueError("fused_rms_rope_qkv_rows: kv_rows must hold B*L entries")
+    wq = weight_q.to(torch.bfloat16).contiguous()
+    wk = weight_k.to(torch.bfloat16).contiguous()
+    cs = _table_for(freqs_cis, L, head_dim, q.device)
+    _lib.check(_lib.lib().fvsr_rms_rope_qkv_rows(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), wq.data_ptr(), wk.data_ptr(), cs.data_ptr(),
+        q.data_ptr(), out_k.data_ptr(), out_v.data_ptr(), kv_rows.data_ptr(), out_k.shape[0],
+        B, L, D, head_dim, float(eps), D, D, D, _lib.stream(q)), "fused_rms_rope_qkv_rows")
+    return q

@@ -42,7 +42,10 @@ from .fp8_linear import convert_linears_fp8, load_fp8_weights, save_fp8_weights
 from .cross_attn import cross_attention
 from .cross_attn import supported as cross_supported
 from .fused_adaln import fused_gate_add, fused_ln_modulate, layer_norm
-from .fused_rms_rope import fused_rms_rope
+from .block import window_token_map
+from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qkv_rows
+from .lcsa.draft import draft_index
+from .lcsa.hip_lcsa import block_sparse_attention_strided
 
 
 def _FLAG(name, default):
@@ -56,6 +59,90 @@ def _unwrap(m):
 
 def _module_eps(m, default=1e-6):
     return getattr(_unwrap(m), "eps", default)
+
+
+def _window_path_on() -> bool:
+    return _FLAG("FS89_WINDOW", "1") and active_backend() == "hip"
+
+
+_MAPS = {}
+
+
+def _window_maps(f, h, w, n_cache_rows, device):
+    """(tok_map, kv_rows, kv_map) for one (f, h, w, cache) geometry: window
+    position -> raster token; raster token -> row of the K/V buffer (after the
+    cached rows); identity over the whole K/V buffer."""
+    key = (f, h, w, n_cache_rows, str(device))
+    m = _MAPS.get(key)
+    if m is None:
+        tok = window_token_map(f, h, w, device=device)
+        inv = torch.empty_like(tok)
+        inv[tok.long()] = torch.arange(tok.numel(), dtype=torch.int32, device=device)
+        kv_rows = (inv + n_cache_rows).contiguous()
+        kv_map = torch.arange(n_cache_rows + tok.numel(), dtype=torch.int32, device=device)
+        m = _MAPS[key] = (tok, kv_rows, kv_map)
+    return m
+
+
+def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream, pre_cache_k,
+                           pre_cache_v, local_range):
+    """The self-attention of integrate.py:42-126 without its layout copies (F2):
+    q stays in raster order and is read through the window map; k and v leave
+    the RMSNorm/RoPE pass directly in window order, behind the cached windows,
+    in the K/V buffer (no partition, no torch.cat of the current chunk); the
+    attention writes its output in raster order (no reverse).  The draft mask
+    is the device one, reading q through the map.  Returns what the reference
+    returns, the caches included (window-ordered [windows, 128, D] views)."""
+    B, L, D = x.shape
+    q = self.q(x).contiguous()
+    k = self.k(x).contiguous()
+    v = self.v(x).contiguous()
+    win = (2, 8, 8)
+    seqlen = f // win[0]
+    block_s = win[0] * win[1] * win[2]
+    one_len = L // block_s // seqlen
+    n_cache = 0 if pre_cache_k is None or pre_cache_v is None else pre_cache_k.shape[0]
+    rows = n_cache * block_s + L
+    kbuf = torch.empty((rows, D), dtype=q.dtype, device=q.device)
+    vbuf = torch.empty((rows, D), dtype=q.dtype, device=q.device)
+    if n_cache:
+        kbuf[:n_cache * block_s].copy_(pre_cache_k.reshape(-1, D))
+        vbuf[:n_cache * block_s].copy_(pre_cache_v.reshape(-1, D))
+    if _module_eps(self.norm_k) != _module_eps(self.norm_q):
+        raise NotImplementedError("q and k RMSNorm eps differ")
+    tok, kv_rows, kv_map = _window_maps(f, h, w, n_cache * block_s, q.device)
+    fused_rms_rope_qkv_rows(q, k, v, _unwrap(self.norm_q).weight, _unwrap(self.norm_k).weight,
+                            freqs, kbuf, vbuf, kv_rows, eps=_module_eps(self.norm_q),
+                            head_dim=self.head_dim)
+    k_w = kbuf.view(-1, block_s, D)
+    v_w = vbuf.view(-1, block_s, D)
+
+    if self.local_attn_mask is None or self.local_attn_mask_h != h // 8 \
+            or self.local_attn_mask_w != w // 8 or self.local_range != local_range:
+        self.local_attn_mask = dit.build_local_block_mask_shifted_vec_normal_slide(
+            h // 8, w // 8, local_range, local_range, include_self=True, device=k_w.device)
+        self.local_attn_mask_h = h // 8
+        self.local_attn_mask_w = w // 8
+        self.local_range = local_range
+    nq = L // block_s
+    index = draft_index(q.view(L, D), k_w, nheads=self.num_heads, q_temporal=seqlen,
+                        local=self.local_attn_mask, topk=topk, nq=nq, q_map=tok)
+    out = torch.empty((L, D), dtype=q.dtype, device=q.device)
+    hd = self.head_dim
+    block_sparse_attention_strided(
+        q.view(L, D), kbuf, vbuf, None, None, heads=self.num_heads, head_dim=hd,
+        q_strides=(D, hd), kv_strides=(D, hd), out=out, o_strides=(D, hd), q_map=tok,
+        kv_map=kv_map, index=index)
+
+    cache_num = k_w.shape[0] // one_len
+    if cache_num > kv_len:
+        cache_k, cache_v = k_w[one_len:], v_w[one_len:]
+    else:
+        cache_k, cache_v = k_w, v_w
+    y = self.o(out.view(B, L, D))
+    if is_stream:
+        return y, cache_k, cache_v
+    return y
 
 
 def _make_self_attn_forward(dit):
@@ -74,6 +161,9 @@ def _make_self_attn_forward(dit):
         assert L == f * h * w, "Sequence length mismatch with provided (f,h,w)."
 
         rope_fn = getattr(dit, "FUSED_ROPE_FN", None)
+        if rope_fn is not None and B == 1 and _window_path_on():
+            return _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream,
+                                          pre_cache_k, pre_cache_v, local_range)
         if rope_fn is not None:
             q = rope_fn(self.q(x), _unwrap(self.norm_q).weight, freqs,
                         eps=_module_eps(self.norm_q), rope=True, head_dim=self.head_dim)

@@ -179,6 +179,23 @@ int fvsr_rms_rope_qk(const void* q, const void* k, const void* wq, const void* w
                      int64_t head_dim, float eps, int64_t ld_in, int64_t ld_out, void* stream);
 
 /*
+ * The self-attention's q/k RMSNorm + RoPE together with the window-order
+ * layout of K and V (F2), replacing integrate.py:59-62 (rope_fn on q and k)
+ * and the WindowPartition3D.partition + KV-cache torch.cat copies of k and v
+ * (integrate.py:70-83): q is normalised and rotated in place (or to out_q,
+ * rows at ld_out); row r of k (normalised and rotated) and of v (copied) go
+ * to row kv_rows[r] of out_k / out_v (ld_kv), the window-ordered K/V buffer
+ * whose first rows the caller filled with the cached windows.  kv_rows int32
+ * [B*L]; rows mapped outside [0, kv_cap) are skipped.  Same shape rules as
+ * fvsr_rms_rope_qk.
+ */
+int fvsr_rms_rope_qkv_rows(const void* q, const void* k, const void* v, const void* wq,
+                           const void* wk, const float* cs, void* out_q, void* out_k,
+                           void* out_v, const int32_t* kv_rows, int64_t kv_cap, int64_t B,
+                           int64_t L, int64_t D, int64_t head_dim, float eps, int64_t ld_in,
+                           int64_t ld_out, int64_t ld_kv, void* stream);
+
+/*
  * Block index from a bool block mask, reference build_csr
  * (flashvsr_sm89_ops/lcsa/triton_lcsa.py:64-71) without its host sync:
  * keep uint8 [H, NQ, NK] -> sel int32 [H, NQ, NK] (kept block ids ascending,
