@@ -84,12 +84,45 @@ def _window_maps(f, h, w, n_cache_rows, device):
     return m
 
 
+def _appendable(t, store, frontier):
+    """t is a contiguous row range of `store` that ends at row `frontier`."""
+    D = store.shape[1]
+    return (t.is_contiguous() and t.device == store.device and t.dtype == store.dtype
+            and t.untyped_storage().data_ptr() == store.untyped_storage().data_ptr()
+            and t.storage_offset() % D == 0 and t.storage_offset() + t.numel() == frontier * D)
+
+
+def _kv_buffers(mod, pre_k, pre_v, cache_rows, L, D, like, grow):
+    """K/V buffers [cache_rows + L, D] whose first rows hold the cached windows.
+    The caches this path returns are views of a per-module store with room
+    after them; when the caller passes them back unchanged (the streaming
+    loop does), the new chunk is appended behind them in place and the cache
+    is not copied (the reference concatenates).  Otherwise, or when the store
+    is full, a new store is made and the cache copied into it once."""
+    st = getattr(mod, "_fs89_kv", None)
+    if st is not None and cache_rows and pre_k is not None and pre_v is not None:
+        sk, sv, fr = st
+        if fr + L <= sk.shape[0] and _appendable(pre_k, sk, fr) and _appendable(pre_v, sv, fr):
+            start = fr - cache_rows
+            mod._fs89_kv = (sk, sv, fr + L)
+            return sk[start:fr + L], sv[start:fr + L]
+    rows = cache_rows + L
+    cap = rows + (4 * L if grow else 0)  # room for a few appended chunks
+    sk = torch.empty((cap, D), dtype=like.dtype, device=like.device)
+    sv = torch.empty((cap, D), dtype=like.dtype, device=like.device)
+    if cache_rows:
+        sk[:cache_rows].copy_(pre_k.reshape(-1, D))
+        sv[:cache_rows].copy_(pre_v.reshape(-1, D))
+    mod._fs89_kv = (sk, sv, rows) if grow else None
+    return sk[:rows], sv[:rows]
+
+
 def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream, pre_cache_k,
                            pre_cache_v, local_range):
     """The self-attention of integrate.py:42-126 without its layout copies (F2):
     q stays in raster order and is read through the window map; k and v leave
     the RMSNorm/RoPE pass directly in window order, behind the cached windows,
-    in the K/V buffer (no partition, no torch.cat of the current chunk); the
+    in the K/V buffer (no partition, no torch.cat; see _kv_buffers); the
     attention writes its output in raster order (no reverse).  The draft mask
     is the device one, reading q through the map.  Returns what the reference
     returns, the caches included (window-ordered [windows, 128, D] views)."""
@@ -102,12 +135,8 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
     block_s = win[0] * win[1] * win[2]
     one_len = L // block_s // seqlen
     n_cache = 0 if pre_cache_k is None or pre_cache_v is None else pre_cache_k.shape[0]
-    rows = n_cache * block_s + L
-    kbuf = torch.empty((rows, D), dtype=q.dtype, device=q.device)
-    vbuf = torch.empty((rows, D), dtype=q.dtype, device=q.device)
-    if n_cache:
-        kbuf[:n_cache * block_s].copy_(pre_cache_k.reshape(-1, D))
-        vbuf[:n_cache * block_s].copy_(pre_cache_v.reshape(-1, D))
+    kbuf, vbuf = _kv_buffers(self, pre_cache_k, pre_cache_v, n_cache * block_s, L, D, q,
+                             is_stream)
     if _module_eps(self.norm_k) != _module_eps(self.norm_q):
         raise NotImplementedError("q and k RMSNorm eps differ")
     tok, kv_rows, kv_map = _window_maps(f, h, w, n_cache * block_s, q.device)

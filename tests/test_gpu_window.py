@@ -133,24 +133,35 @@ def test_window_path_equals_copy_path(monkeypatch, hw):
     g = torch.Generator().manual_seed(5)
     attn = dit.SelfAttention(g).to(dev)
     kv_len, topk = 2, 3
-    chunks = [(6, torch.randn(1, 6 * h * w, D, generator=g)), (2, torch.randn(1, 2 * h * w, D, generator=g))]
-    res = {}
+    # 6 latent frames, then 2-frame steps with the cache; step 3 passes a copy
+    # of the cache (not the store's view), which must take the copying route.
+    chunks = [(6, torch.randn(1, 6 * h * w, D, generator=g))] + [
+        (2, torch.randn(1, 2 * h * w, D, generator=g)) for _ in range(4)]
+    res, stores = {}, []
     for mode in ("0", "1"):
         monkeypatch.setenv("FS89_WINDOW", mode)
         attn.local_attn_mask = None
+        attn._fs89_kv = None
         ck = cv = None
         outs = []
-        for f, x in chunks:
+        for i, (f, x) in enumerate(chunks):
             x = x.to(torch.bfloat16).to(dev)
-            fr = _freqs(f * h * w, dev) if mode == "0" else res.get(("fr", f))
-            res[("fr", f)] = fr
+            fr = _freqs(f * h * w, dev) if ("fr", i) not in res else res[("fr", i)]
+            res[("fr", i)] = fr
+            if i == 3:
+                ck, cv = ck.clone(), cv.clone()
             with torch.no_grad():
                 y, ck, cv = attn(x, fr, f, h, w, None, topk, kv_len=kv_len, is_stream=True,
                                  pre_cache_k=ck, pre_cache_v=cv)
+            if mode == "1":
+                stores.append(ck.untyped_storage().data_ptr())
             outs.append((y.clone(), ck.clone(), cv.clone()))
         res[mode] = outs
     torch.cuda.synchronize()
-    assert len(taken) == 2  # the window path served both chunks of mode "1" only
+    assert len(taken) == len(chunks)  # the window path served mode "1" only
+    # appended in place at steps 1, 2 and 4; a new store at step 3 (foreign cache)
+    assert stores[1] == stores[0] and stores[2] == stores[0]
+    assert stores[3] != stores[0] and stores[4] == stores[3]
     for (y0, k0, v0), (y1, k1, v1) in zip(res["0"], res["1"]):
         assert k0.shape == k1.shape and v0.shape == v1.shape
         assert torch.equal(k0, k1) and torch.equal(v0, v1)
