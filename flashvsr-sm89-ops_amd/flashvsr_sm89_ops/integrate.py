@@ -65,6 +65,15 @@ def _window_path_on() -> bool:
     return _FLAG("FS89_WINDOW", "1") and active_backend() == "hip"
 
 
+def _window_path_ok(x, f, h, w, head_dim) -> bool:
+    """Shapes the copy-free path serves: batch 1, bf16 on the GPU, whole
+    2x8x8 windows, head_dim 128, a hidden size the fused kernels take."""
+    B, L, D = x.shape
+    return (B == 1 and x.dtype == torch.bfloat16 and x.is_cuda and head_dim == 128
+            and f % 2 == 0 and h % 8 == 0 and w % 8 == 0 and L == f * h * w
+            and D % head_dim == 0 and D <= 1536)
+
+
 _MAPS = {}
 
 
@@ -190,7 +199,7 @@ def _make_self_attn_forward(dit):
         assert L == f * h * w, "Sequence length mismatch with provided (f,h,w)."
 
         rope_fn = getattr(dit, "FUSED_ROPE_FN", None)
-        if rope_fn is not None and B == 1 and _window_path_on():
+        if rope_fn is not None and _window_path_ok(x, f, h, w, self.head_dim) and _window_path_on():
             return _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream,
                                           pre_cache_k, pre_cache_v, local_range)
         if rope_fn is not None:

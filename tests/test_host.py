@@ -392,3 +392,24 @@ def test_enable_loads_stored_fp8_weights(tmp_path, monkeypatch):
     assert applied["fp8_weights"] == "loaded" and applied["fp8_linears"] == 8
     assert torch.equal(pipe.model.blocks[1].self_attn.o.weight.view(torch.uint8),
                        src.blocks[1].self_attn.o.weight.view(torch.uint8))
+
+
+def test_window_path_shape_guard():
+    """The copy-free self-attention path (F2) takes batch-1 bf16 GPU input in
+    whole 2x8x8 windows only; anything else keeps the reference's sequence."""
+    from flashvsr_sm89_ops.integrate import _window_path_ok
+    x = torch.empty(1, 2 * 16 * 24, 256, dtype=torch.bfloat16)
+    assert not _window_path_ok(x, 2, 16, 24, 128)          # on the CPU
+    meta = torch.empty(1, 2 * 16 * 24, 256, dtype=torch.bfloat16, device="meta")
+    # a stand-in exposing is_cuda, so the shape rules can be checked without a GPU
+    class T:
+        def __init__(self, shape, dtype=torch.bfloat16):
+            self.shape, self.dtype, self.is_cuda = shape, dtype, True
+    assert _window_path_ok(T((1, 768, 256)), 2, 16, 24, 128)
+    assert not _window_path_ok(T((2, 768, 256)), 2, 16, 24, 128)           # batch 2
+    assert not _window_path_ok(T((1, 768, 256), torch.float32), 2, 16, 24, 128)
+    assert not _window_path_ok(T((1, 3 * 16 * 24, 256)), 3, 16, 24, 128)  # odd frames
+    assert not _window_path_ok(T((1, 2 * 12 * 24, 256)), 2, 12, 24, 128)  # h % 8
+    assert not _window_path_ok(T((1, 768, 256)), 2, 16, 24, 64)            # head_dim
+    assert not _window_path_ok(T((1, 768, 3072)), 2, 16, 24, 128)          # D > 1536
+    del meta
