@@ -400,7 +400,6 @@ def test_window_path_shape_guard():
     from flashvsr_sm89_ops.integrate import _window_path_ok
     x = torch.empty(1, 2 * 16 * 24, 256, dtype=torch.bfloat16)
     assert not _window_path_ok(x, 2, 16, 24, 128)          # on the CPU
-    meta = torch.empty(1, 2 * 16 * 24, 256, dtype=torch.bfloat16, device="meta")
     # a stand-in exposing is_cuda, so the shape rules can be checked without a GPU
     class T:
         def __init__(self, shape, dtype=torch.bfloat16):
@@ -412,4 +411,3 @@ def test_window_path_shape_guard():
     assert not _window_path_ok(T((1, 2 * 12 * 24, 256)), 2, 12, 24, 128)  # h % 8
     assert not _window_path_ok(T((1, 768, 256)), 2, 16, 24, 64)            # head_dim
     assert not _window_path_ok(T((1, 768, 3072)), 2, 16, 24, 128)          # D > 1536
-    del meta
