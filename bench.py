@@ -397,7 +397,127 @@ def components(torch, fv):
                             "attn_frac_bf16": fl_a / (t_a * 1e-3) / PEAK["bf16"],
                             "gemm_GFLOP": fl_g / 1e9, "attn_GFLOP": fl_a / 1e9}
     del xs
+    out["enable_block_step"] = enable_block_step(torch, fv, dev)
     return out
+
+
+def enable_block_step(torch, fv, dev):
+    """One DiT block through the forwards enable() installs, one streaming step
+    at the C5 geometry (f=2, 48x88 latent, cache of 2 time rows), per-token x
+    per-channel FP8 q/k/v/o and FFN, draft top-k 30%: the fused dataflow
+    (FS89_WINDOW=1) against the reference's (FS89_WINDOW=0).  The
+    cross-attention is a stand-in returning a fixed tensor (F3 is timed above)."""
+    import types
+    from flashvsr_sm89_ops import integrate
+    from flashvsr_sm89_ops.fp8_ffn import FP8FFN
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    from flashvsr_sm89_ops.lcsa.draft import generate_draft_block_mask
+    from flashvsr_sm89_ops.lcsa.masks import local_block_mask
+    from flashvsr_sm89_ops.rope import wan_freqs_cis
+    from flashvsr_sm89_ops.compat_bsa import _hip_block_sparse_attn_func
+    g = torch.Generator().manual_seed(3)
+    f2, h2, w2 = 2, 48, 88
+    Ls = f2 * h2 * w2
+
+    def lin(n, k):
+        m = torch.nn.Linear(k, n, dtype=torch.bfloat16)
+        with torch.no_grad():
+            m.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
+            m.bias.zero_()
+        return FP8Linear(m.to(dev), per_channel=True, per_token=True)
+
+    def part(x, win):
+        B, f, h, w, C = x.shape
+        return x.view(B, f // 2, 2, h // 8, 8, w // 8, 8, C).permute(
+            0, 1, 3, 5, 2, 4, 6, 7).reshape(-1, 128, C)
+
+    def rev(x, win, fhw):
+        f, h, w = fhw
+        C = x.shape[-1]
+        return x.view(1, f // 2, h // 8, w // 8, 2, 8, 8, C).permute(
+            0, 1, 4, 2, 5, 3, 6, 7).reshape(1, f, h, w, C)
+
+    loc = torch.from_numpy(local_block_mask(6, 11, 7)).to(dev)
+
+    class SelfAttention(torch.nn.Module):
+        def forward(self, x, freqs, f=None, h=None, w=None, local_num=None, topk=None,
+                    train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                    is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+            raise AssertionError
+
+        def attn(self, q, k, v, mask):
+            return _hip_block_sparse_attn_func(
+                q[0].view(-1, HEADS, HD), k[0].view(-1, HEADS, HD), v[0].view(-1, HEADS, HD),
+                None, None, None, None, mask, q.shape[1], k.shape[1]).reshape(1, -1, DIM)
+
+    class CrossAttention(torch.nn.Module):
+        def forward(self, x, y, is_stream=False):
+            raise AssertionError
+
+    class DiTBlock(torch.nn.Module):
+        def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
+                    train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                    is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+            raise AssertionError
+
+    dit = types.SimpleNamespace(
+        SelfAttention=SelfAttention, CrossAttention=CrossAttention, DiTBlock=DiTBlock,
+        WindowPartition3D=types.SimpleNamespace(partition=part, reverse=rev),
+        build_local_block_mask_shifted_vec_normal_slide=lambda *a, **k: loc,
+        generate_draft_block_mask=generate_draft_block_mask, modulate=None)
+
+    class Pipe:
+        model = torch.nn.Module()
+
+        def denoising_model(self):
+            return self.model
+    env0 = {k: os.environ.get(k) for k in ("FS89_FP8", "FS89_DRAFT", "FS89_WINDOW")}
+    os.environ["FS89_FP8"], os.environ["FS89_DRAFT"] = "", "1"
+    fv.enable(Pipe(), dit_module=dit, verbose=False)
+    blk = DiTBlock()
+    sa = blk.self_attn = SelfAttention()
+    sa.num_heads, sa.head_dim = HEADS, HD
+    for n in ("q", "k", "v", "o"):
+        setattr(sa, n, lin(DIM, DIM))
+    nw = torch.nn.Module()
+    nw.weight = torch.nn.Parameter((1 + 0.1 * torch.randn(DIM, generator=g)).to(torch.bfloat16).to(dev))
+    nw.eps = 1e-6
+    sa.norm_q = sa.norm_k = nw
+    sa.local_attn_mask = None
+    sa.local_attn_mask_h = sa.local_attn_mask_w = sa.local_range = None
+    blk.modulation = (0.1 * torch.randn(1, 6, DIM, generator=g)).to(torch.bfloat16).to(dev)
+    blk.norm1 = torch.nn.LayerNorm(DIM, eps=1e-6, elementwise_affine=False)
+    blk.norm2 = torch.nn.LayerNorm(DIM, eps=1e-6, elementwise_affine=False)
+    blk.norm3 = torch.nn.LayerNorm(DIM, eps=1e-6, dtype=torch.bfloat16).to(dev)
+    blk.ffn = FP8FFN(lin(FFN, DIM), lin(DIM, FFN))
+    yc = (0.1 * torch.randn(1, Ls, DIM, generator=g)).to(torch.bfloat16).to(dev)
+    blk.cross_attn = lambda x, ctx, is_stream=False: yc
+    t_mod = (0.1 * torch.randn(1, 6, DIM, generator=g)).to(torch.bfloat16).to(dev)
+    fr = wan_freqs_cis(f2, h2, w2, HD).to(dev)
+    topk = int(0.3 * 66 * 3 * 66)
+    xs = [(torch.randn(1, Ls, DIM, generator=g)).to(torch.bfloat16).to(dev) for _ in range(2)]
+    res = {}
+    for mode in ("0", "1"):
+        os.environ["FS89_WINDOW"] = mode
+        sa._fs89_kv = None
+        ck = (torch.randn(2 * 66, 128, DIM, generator=g)).to(torch.bfloat16).to(dev)
+        cv = ck.clone()
+        state = {"ck": ck, "cv": cv}
+
+        def step(i):
+            with torch.no_grad():
+                _, state["ck"], state["cv"] = blk(
+                    xs[i], None, t_mod, fr, f2, h2, w2, None, topk, kv_len=2, is_stream=True,
+                    pre_cache_k=state["ck"], pre_cache_v=state["cv"])
+        res[mode] = timeit(torch, step, 2, iters=10)
+    for k, v in env0.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
+    return {"reference_dataflow_ms": res["0"], "fused_ms": res["1"],
+            "saved_ms_per_chunk_30_blocks": 30 * (res["0"] - res["1"]),
+            "geometry": "f=2, 48x88 latent, 132-window cache, top-k 30% of 3 time rows"}
 
 
 def cpu_baseline(args):

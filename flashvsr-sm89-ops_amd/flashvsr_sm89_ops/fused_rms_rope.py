@@ -113,7 +113,8 @@ def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """The self-attention's RMSNorm + RoPE of q and k (integrate.py:59-62)
     with k and v written straight into a window-ordered K/V buffer
     (integrate.py:70-83 without the partition and cat copies).  q, k, v:
-    [B, L, D] bf16 with contiguous rows; q is rotated in place and returned;
+    [B, L, D] bf16 with unit-stride rows sharing one row stride (contiguous
+    tensors or column slices of a fused qkv); q is rotated in place and returned;
     row r of k and v goes to row ``kv_rows[r]`` of ``out_k`` / ``out_v``
     ([rows, D] bf16, contiguous)."""
     _lib.require_gpu(q, k, v, weight_q, weight_k, out_k, out_v, kv_rows)
@@ -123,8 +124,11 @@ def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     B, L, D = q.shape
     if k.shape != q.shape or v.shape != q.shape:
         raise ValueError("fused_rms_rope_qkv_rows: q, k, v shapes differ")
-    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
-        raise ValueError("fused_rms_rope_qkv_rows: q, k, v must be contiguous")
+    ld = q.stride(1)
+    for t in (q, k, v):
+        if t.stride(-1) != 1 or t.stride(1) != ld or (B > 1 and t.stride(0) != L * ld):
+            raise ValueError("fused_rms_rope_qkv_rows: q, k, v need unit-stride rows with one "
+                             "common row stride (e.g. column slices of a fused qkv)")
     if out_k.shape != out_v.shape or out_k.dim() != 2 or out_k.shape[1] != D or \
             not (out_k.is_contiguous() and out_v.is_contiguous()):
         raise ValueError("fused_rms_rope_qkv_rows: out_k/out_v must be contiguous [rows, D]")
@@ -136,5 +140,5 @@ def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     _lib.check(_lib.lib().fvsr_rms_rope_qkv_rows(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), wq.data_ptr(), wk.data_ptr(), cs.data_ptr(),
         q.data_ptr(), out_k.data_ptr(), out_v.data_ptr(), kv_rows.data_ptr(), out_k.shape[0],
-        B, L, D, head_dim, float(eps), D, D, D, _lib.stream(q)), "fused_rms_rope_qkv_rows")
+        B, L, D, head_dim, float(eps), ld, ld, D, _lib.stream(q)), "fused_rms_rope_qkv_rows")
     return q

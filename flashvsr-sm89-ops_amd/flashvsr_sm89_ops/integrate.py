@@ -38,10 +38,14 @@ import torch
 
 from .compat_bsa import active_backend, ensure_bsa_available
 from .fp8_ffn import convert_ffn_fp8
-from .fp8_linear import convert_linears_fp8, load_fp8_weights, save_fp8_weights
+from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm, load_fp8_weights, save_fp8_weights
+from .fp8_quant import quantize_fp8
 from .cross_attn import cross_attention
 from .cross_attn import supported as cross_supported
-from .fused_adaln import fused_gate_add, fused_ln_modulate, layer_norm
+from .fused_adaln import (fused_gate_add, fused_gate_add_ln_modulate_quant, fused_ln_modulate,
+                          fused_ln_modulate_quant, layer_norm)
+from .cross_attn import unit_gate
+from .fp8_ffn import FP8FFN, gemm_gelu_quant_fp8
 from .block import window_token_map
 from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qkv_rows
 from .lcsa.draft import draft_index
@@ -126,8 +130,35 @@ def _kv_buffers(mod, pre_k, pre_v, cache_rows, L, D, like, grow):
     return sk[:rows], sv[:rows]
 
 
+def _qkv_fused(mod):
+    """One [3D, D] e4m3 weight for the q, k and v FP8Linears (built once per
+    module, rebuilt if any of them changes): the three projections of the
+    same activations become one GEMM on one quantisation of them (the
+    reference quantises the input three times).  Per-tensor weight scales
+    become per-column vectors of the same value, which the GEMM epilogue
+    applies with the same arithmetic.  None when the three cannot share."""
+    lins = [getattr(mod, n, None) for n in ("q", "k", "v")]
+    if not all(isinstance(l, FP8Linear) for l in lins):
+        return None
+    if len({l.per_token for l in lins}) != 1 or len({l.in_features for l in lins}) != 1:
+        return None
+    if len({l.bias is None for l in lins}) != 1:
+        return None
+    key = tuple((l.weight.data_ptr(), l.weight._version, l.w_scale.data_ptr(), l.w_scale._version,
+                 None if l.bias is None else (l.bias.data_ptr(), l.bias._version)) for l in lins)
+    c = getattr(mod, "_fs89_qkv", None)
+    if c is not None and c[0] == key:
+        return c[1]
+    w3 = torch.cat([l.weight for l in lins]).contiguous()
+    s3 = torch.cat([l.w_scale.float().reshape(-1).expand(l.out_features) for l in lins]).contiguous()
+    b3 = None if lins[0].bias is None else torch.cat([l.bias for l in lins]).contiguous()
+    val = (w3, s3, b3, lins[0].per_token)
+    mod._fs89_qkv = (key, val)
+    return val
+
+
 def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream, pre_cache_k,
-                           pre_cache_v, local_range):
+                           pre_cache_v, local_range, x8s=None):
     """The self-attention of integrate.py:42-126 without its layout copies (F2):
     q stays in raster order and is read through the window map; k and v leave
     the RMSNorm/RoPE pass directly in window order, behind the cached windows,
@@ -136,9 +167,19 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
     is the device one, reading q through the map.  Returns what the reference
     returns, the caches included (window-ordered [windows, 128, D] views)."""
     B, L, D = x.shape
-    q = self.q(x).contiguous()
-    k = self.k(x).contiguous()
-    v = self.v(x).contiguous()
+    fq = _qkv_fused(self)
+    if fq is not None:
+        w3, s3, b3, per_token = fq
+        if x8s is None:
+            x8s = quantize_fp8(x.reshape(-1, D), per_token=per_token)
+        qkv = fp8_gemm(x8s[0], x8s[1], w3, s3, b3)  # [L, 3D]: q, k, v column slices
+        q, k, v = (qkv[:, i * D:(i + 1) * D].view(B, L, D) for i in range(3))
+    else:
+        if x8s is not None:
+            raise ValueError("activation codes given but q/k/v are not FP8 linears")
+        q = self.q(x).contiguous()
+        k = self.k(x).contiguous()
+        v = self.v(x).contiguous()
     win = (2, 8, 8)
     seqlen = f // win[0]
     block_s = win[0] * win[1] * win[2]
@@ -163,13 +204,14 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
         self.local_attn_mask_w = w // 8
         self.local_range = local_range
     nq = L // block_s
-    index = draft_index(q.view(L, D), k_w, nheads=self.num_heads, q_temporal=seqlen,
+    q2 = q.reshape(L, D)  # a view (rows may be strided: column slice of the fused qkv)
+    index = draft_index(q2, k_w, nheads=self.num_heads, q_temporal=seqlen,
                         local=self.local_attn_mask, topk=topk, nq=nq, q_map=tok)
     out = torch.empty((L, D), dtype=q.dtype, device=q.device)
     hd = self.head_dim
     block_sparse_attention_strided(
-        q.view(L, D), kbuf, vbuf, None, None, heads=self.num_heads, head_dim=hd,
-        q_strides=(D, hd), kv_strides=(D, hd), out=out, o_strides=(D, hd), q_map=tok,
+        q2, kbuf, vbuf, None, None, heads=self.num_heads, head_dim=hd,
+        q_strides=(q2.stride(0), hd), kv_strides=(D, hd), out=out, o_strides=(D, hd), q_map=tok,
         kv_map=kv_map, index=index)
 
     cache_num = k_w.shape[0] // one_len
@@ -309,6 +351,21 @@ def _affine_layer_norm(m):
     return w, b, m.eps
 
 
+def _row_codes_block(dit, blk, x, f, h, w) -> bool:
+    """The DiT block runs the per-token FP8 dataflow of the C5 block (AdaLN
+    writing codes, one q/k/v GEMM, the copy-free self-attention): fused AdaLN
+    and RoPE on, the HIP attention, per-token q/k/v FP8 linears, batch-1 bf16
+    input in whole windows."""
+    sa = getattr(blk, "self_attn", None)
+    if sa is None or getattr(dit, "FUSED_ADALN", None) is None or \
+            getattr(dit, "FUSED_ROPE_FN", None) is None:
+        return False
+    if not (_window_path_on() and _window_path_ok(x, f, h, w, getattr(sa, "head_dim", 0))):
+        return False
+    fq = _qkv_fused(sa)
+    return fq is not None and fq[3]
+
+
 def _make_dit_block_forward(dit):
     """Fused-aware copy of upstream DiTBlock.forward (integrate.py:148-184)."""
 
@@ -320,13 +377,24 @@ def _make_dit_block_forward(dit):
         fa = getattr(dit, "FUSED_ADALN", None)
         if fa is not None:
             ln_mod, gate_add = fa
-            input_x = ln_mod(x, scale_msa, shift_msa, eps=_module_eps(self.norm1))
+        rows = _row_codes_block(dit, self, x, f, h, w)
+        if rows:
+            # Per-token FP8 throughout: the AdaLN writes the codes the fused
+            # q/k/v GEMM takes (no bf16 round trip, one quantisation).
+            x8s = fused_ln_modulate_quant(x, scale_msa, shift_msa, eps=_module_eps(self.norm1))
+            r = _window_self_attention(dit, self.self_attn, x, freqs, f, h, w, topk, kv_len,
+                                       is_stream, pre_cache_k, pre_cache_v, local_range, x8s=x8s)
+            self_attn_output, self_attn_cache_k, self_attn_cache_v = (
+                r if is_stream else (r, None, None))
         else:
-            input_x = dit.modulate(self.norm1(x), shift_msa, scale_msa)
-        self_attn_output, self_attn_cache_k, self_attn_cache_v = self.self_attn(
-            input_x, freqs, f, h, w, local_num, topk, train_img, block_id,
-            kv_len=kv_len, is_full_block=is_full_block, is_stream=is_stream,
-            pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v, local_range=local_range)
+            if fa is not None:
+                input_x = ln_mod(x, scale_msa, shift_msa, eps=_module_eps(self.norm1))
+            else:
+                input_x = dit.modulate(self.norm1(x), shift_msa, scale_msa)
+            self_attn_output, self_attn_cache_k, self_attn_cache_v = self.self_attn(
+                input_x, freqs, f, h, w, local_num, topk, train_img, block_id,
+                kv_len=kv_len, is_full_block=is_full_block, is_stream=is_stream,
+                pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v, local_range=local_range)
 
         if fa is not None:
             x = gate_add(x, gate_msa, self_attn_output)
@@ -337,7 +405,20 @@ def _make_dit_block_forward(dit):
             normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2])
         else:
             normed = self.norm3(x)
-        x = x + self.cross_attn(normed, context, is_stream=is_stream)
+        yc = self.cross_attn(normed, context, is_stream=is_stream)
+        if rows and isinstance(self.ffn, FP8FFN) and yc.shape == x.shape and yc.is_contiguous():
+            # x + cross-attention output and the FFN's AdaLN in one pass (a
+            # unit gate), its per-token codes straight into the FFN's GEMMs.
+            B, L, D = x.shape
+            x, h8, hs = fused_gate_add_ln_modulate_quant(
+                x, unit_gate(D, x.device), yc, scale_mlp, shift_mlp, eps=_module_eps(self.norm2))
+            g8, gs = gemm_gelu_quant_fp8(h8, hs, self.ffn.lin0, True)
+            yf = self.ffn.lin2._mm(g8, gs)
+            x = gate_add(x, gate_mlp, yf.view(B, L, -1))
+            if is_stream:
+                return x, self_attn_cache_k, self_attn_cache_v
+            return x
+        x = x + yc
         if fa is not None:
             input_x = ln_mod(x, scale_mlp, shift_mlp, eps=_module_eps(self.norm2))
         else:

@@ -203,3 +203,99 @@ def test_qkv_rows_kernel_matches_partition():
     assert torch.equal(kbuf[ncache:][~skip], want_k[~skip])
     assert torch.equal(vbuf[ncache:][~skip], want_v[~skip])
     assert (kbuf[:ncache] == 7).all() and (kbuf[ncache:][skip] == 7).all()
+
+
+def _fake_block_dit(per_token, g, ffn_dim=512):
+    """The window test's DiT plus a DiTBlock whose q/k/v/o and FFN are the FP8
+    modules enable() installs (per-channel weights; per-token or per-tensor
+    activations), a stand-in cross-attention and the upstream norms."""
+    from flashvsr_sm89_ops.fp8_ffn import FP8FFN
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    dit = _fake_dit()
+    SA = dit.SelfAttention
+
+    def fp8(n, k):
+        lin = torch.nn.Linear(k, n, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(n, k, generator=g) * 0.05)
+            lin.bias.copy_(torch.randn(n, generator=g) * 0.02)
+        return FP8Linear(lin.cuda(), per_channel=True, per_token=per_token)
+
+    class DiTBlock(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.self_attn = SA(g)
+            for n in ("q", "k", "v", "o"):
+                setattr(self.self_attn, n, fp8(D, D))
+            self.modulation = torch.nn.Parameter(
+                (torch.randn(1, 6, D, generator=g) * 0.1).to(torch.bfloat16))
+            self.norm1 = torch.nn.LayerNorm(D, eps=1e-6, elementwise_affine=False)
+            self.norm2 = torch.nn.LayerNorm(D, eps=1e-6, elementwise_affine=False)
+            self.norm3 = torch.nn.LayerNorm(D, eps=1e-6, dtype=torch.bfloat16)
+            with torch.no_grad():
+                self.norm3.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+                self.norm3.bias.copy_(0.1 * torch.randn(D, generator=g))
+            self.ffn = FP8FFN(fp8(ffn_dim, D), fp8(D, ffn_dim))
+
+        def cross_attn(self, x, ctx, is_stream=False):
+            return (x * 0.5 + 0.25).contiguous()
+
+        def gate(self, x, gate, residual):
+            return x + gate * residual
+
+        def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
+                    train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                    is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+            raise AssertionError("rebound by enable()")
+
+    dit.DiTBlock = DiTBlock
+    return dit
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+def test_fused_block_equals_reference_dataflow(monkeypatch, per_token):
+    """The rebound DiTBlock with the copy-free self-attention, one q/k/v GEMM
+    on one quantisation (and, per token, the AdaLN writing the codes and the
+    cross residual fused with the FFN's AdaLN) equals the reference's dataflow
+    (FS89_WINDOW=0: three quantisations, three GEMMs, bf16 AdaLN outputs,
+    partition/cat/reverse) bit for bit over a streaming run."""
+    import flashvsr_sm89_ops as fv
+    from flashvsr_sm89_ops import integrate
+    h, w = 16, 24
+    g = torch.Generator().manual_seed(9)
+    dit = _fake_block_dit(per_token, g)
+    monkeypatch.setenv("FS89_FP8", "")
+    monkeypatch.setenv("FS89_DRAFT", "1")
+    fv.enable(_Pipe(), dit_module=dit, verbose=False)
+    blk = dit.DiTBlock().cuda()
+    calls = []
+    real = integrate.fused_ln_modulate_quant
+
+    def spy(*a, **k):
+        calls.append(1)
+        return real(*a, **k)
+    monkeypatch.setattr(integrate, "fused_ln_modulate_quant", spy)
+    t_mod = (torch.randn(1, 6, D, generator=g) * 0.1).to(torch.bfloat16).cuda()
+    chunks = [(6, torch.randn(1, 6 * h * w, D, generator=g))] + [
+        (2, torch.randn(1, 2 * h * w, D, generator=g)) for _ in range(2)]
+    frs = [_freqs(f * h * w, "cuda") for f, _ in chunks]
+    res = {}
+    for mode in ("0", "1"):
+        monkeypatch.setenv("FS89_WINDOW", mode)
+        blk.self_attn.local_attn_mask = None
+        blk.self_attn._fs89_kv = None
+        ck = cv = None
+        outs = []
+        for (f, x), fr in zip(chunks, frs):
+            x = x.to(torch.bfloat16).cuda()
+            with torch.no_grad():
+                y, ck, cv = blk(x, None, t_mod, fr, f, h, w, None, 3, kv_len=2, is_stream=True,
+                                pre_cache_k=ck, pre_cache_v=cv)
+            outs.append((y.clone(), ck.clone(), cv.clone()))
+        res[mode] = outs
+    torch.cuda.synchronize()
+    assert len(calls) == (3 if per_token else 0)  # the fused AdaLN served the per-token run only
+    for (y0, k0, v0), (y1, k1, v1) in zip(res["0"], res["1"]):
+        assert torch.isfinite(y0.float()).all()
+        assert torch.equal(k0, k1) and torch.equal(v0, v1)
+        assert torch.equal(y0, y1)
