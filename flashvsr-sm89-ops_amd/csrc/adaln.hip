@@ -281,11 +281,16 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_generic(
 // in fp32, y = bf16(w * ((x - mean) * rstd) + b) in fp32 with
 // rstd = rsqrt(var + eps), one rounding.  R rows per wavefront, rows in
 // registers as in ln_modulate_vec; optional per-row e4m3 codes of y.
-template <int VPL, int R, bool WRITE_OUT, bool QUANT>
+// GATE: the rows are first x1 = bf16(x + bf16(gate * res)) (fused_gate_add,
+// gate [B, 1, D] per batch element of L rows), written to x1_out, then
+// normalised from the registers.
+template <int VPL, int R, bool WRITE_OUT, bool QUANT, bool GATE = false>
 __global__ __launch_bounds__(kThreads) void layer_norm_vec(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ out, int64_t rows, int64_t D,
-    float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
+    float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale,
+    const uint16_t* __restrict__ gate = nullptr, const uint16_t* __restrict__ res = nullptr,
+    uint16_t* __restrict__ x1_out = nullptr, int64_t L = 1) {
   const int lane = threadIdx.x & 63;
   const int64_t r0 = ((int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
   if (r0 >= rows) return;
@@ -304,6 +309,31 @@ __global__ __launch_bounds__(kThreads) void layer_norm_vec(
     const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
     wraw[j] = *(const u32x4_t*)(w + cc * 8);
     braw[j] = *(const u32x4_t*)(bias + cc * 8);
+  }
+  if (GATE) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t pg = (row[r] / L) * D;
+      u32x4_t rraw[VPL], graw[VPL];
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+        const int64_t cc = clamp_chunk(lane + 64 * j, nchunk);
+        rraw[j] = *(const u32x4_t*)(res + row[r] * D + cc * 8);
+        graw[j] = *(const u32x4_t*)(gate + pg + cc * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < VPL; ++j) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t t = pack_bf16x2_once(bf_lo(graw[j][p]) * bf_lo(rraw[j][p]),
+                                              bf_hi(graw[j][p]) * bf_hi(rraw[j][p]));
+          raw[r][j][p] = pack_bf16x2_once(bf_lo(raw[r][j][p]) + bf_lo(t),
+                                          bf_hi(raw[r][j][p]) + bf_hi(t));
+        }
+        const int64_t c = lane + 64 * j;
+        if (c < nchunk && r0 + r < rows) *(u32x4_t*)(x1_out + row[r] * D + c * 8) = raw[r][j];
+      }
+    }
   }
   float v[R][VPL][8], sum[R];
 #pragma unroll
@@ -571,5 +601,38 @@ extern "C" int fvsr_gate_add(const void* x, const void* gate, const void* res, v
     hipLaunchKernelGGL(gate_add_generic, dim3((unsigned)blocks), dim3(kThreads), 0, st, xp, gp,
                        rp, op, n, L * D, D);
   }
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_gate_add_layer_norm(const void* x, const void* gate, const void* res,
+                                        void* x1, const void* weight, const void* bias,
+                                        void* out, int64_t B, int64_t L, int64_t D, float eps,
+                                        void* codes, float* row_scale, void* stream) {
+  if (B < 0 || L < 0 || D <= 0) return FVSR_EINVAL;
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!x || !gate || !res || !x1 || !weight || !bias || (!out && !codes) ||
+      (codes && !row_scale))
+    return FVSR_EINVAL;
+  const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(gate) &&
+                   aligned16(res) && aligned16(x1) && aligned16(weight) && aligned16(bias) &&
+                   (!out || aligned16(out)) && (!codes || aligned16(codes));
+  if (!vec) return FVSR_EUNSUPPORTED;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t *xp = (const uint16_t*)x, *gp = (const uint16_t*)gate, *rp = (const uint16_t*)res,
+                 *wp = (const uint16_t*)weight, *bp = (const uint16_t*)bias;
+  uint16_t *x1p = (uint16_t*)x1, *op = (uint16_t*)out;
+  uint8_t* qp = (uint8_t*)codes;
+  const int64_t groups = (rows + kLnRows - 1) / kLnRows;
+  const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves)), block(kThreads);
+  if (out && codes)
+    hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, true, true, true>), vgrid, block, 0, st, xp, wp,
+                       bp, op, rows, D, eps, qp, row_scale, gp, rp, x1p, L);
+  else if (out)
+    hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, true, false, true>), vgrid, block, 0, st, xp,
+                       wp, bp, op, rows, D, eps, qp, row_scale, gp, rp, x1p, L);
+  else
+    hipLaunchKernelGGL((layer_norm_vec<3, kLnRows, false, true, true>), vgrid, block, 0, st, xp,
+                       wp, bp, op, rows, D, eps, qp, row_scale, gp, rp, x1p, L);
   return fvsr_launch_status();
 }

@@ -46,6 +46,8 @@ _SIGS = {
     "fvsr_layer_norm": ([_P, _P, _P, _P, _I64, _I64, _F, _P, _P, _P], _I),
     "fvsr_gate_add_ln_modulate": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P],
                                   _I),
+    "fvsr_gate_add_layer_norm": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _F, _P, _P, _P],
+                                 _I),
     "fvsr_rms_rope": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P], _I),
     "fvsr_rms_rope_qk": ([_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F, _I64, _I64,
                           _P], _I),

@@ -99,6 +99,34 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
     return out
 
 
+def fused_gate_add_layer_norm(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor,
+                              weight: torch.Tensor, bias: torch.Tensor | None,
+                              eps: float = 1e-6):
+    """x1 = fused_gate_add(x, gate, residual) and layer_norm(x1, weight, bias)
+    in one pass over the rows: the self-attention's gated residual and the
+    norm3 before the cross-attention (integrate.py:151-171).  x, residual
+    [B, L, D] bf16 (residual may be a [B*L, D] view), gate [B, 1, D].
+    Returns (x1, normed), each [B, L, D] bf16, equal to the two-step results."""
+    B, L, D = x.shape
+    res = residual.reshape(B, L, D)
+    for t in (x, res, gate):
+        if not t.is_contiguous():
+            raise ValueError("fused_gate_add_layer_norm: tensors must be contiguous")
+    _lib.require_gpu(x, res, gate)
+    _lib.require_dtype(res, torch.bfloat16, "residual")
+    _lib.require_dtype(gate, torch.bfloat16, "gate")
+    if tuple(gate.shape) != (B, 1, D):
+        raise ValueError(f"gate must be [{B}, 1, {D}], got {tuple(gate.shape)}")
+    x2, w, b = _ln_affine_args(x, weight, bias)
+    x1 = torch.empty_like(x2)
+    out = torch.empty_like(x2)
+    _lib.check(_lib.lib().fvsr_gate_add_layer_norm(
+        x2.data_ptr(), gate.data_ptr(), res.data_ptr(), x1.data_ptr(), w.data_ptr(), b.data_ptr(),
+        out.data_ptr(), B, L, D, float(eps), None, None, _lib.stream(x2)),
+        "fused_gate_add_layer_norm")
+    return x1, out
+
+
 def layer_norm_quant(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None,
                      eps: float = 1e-6, write_bf16: bool = False):
     """layer_norm + per-row e4m3 quantisation of its output in one pass.

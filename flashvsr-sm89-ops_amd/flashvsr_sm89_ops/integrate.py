@@ -42,7 +42,8 @@ from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm, load_fp8_weigh
 from .fp8_quant import quantize_fp8
 from .cross_attn import cross_attention
 from .cross_attn import supported as cross_supported
-from .fused_adaln import (fused_gate_add, fused_gate_add_ln_modulate_quant, fused_ln_modulate,
+from .fused_adaln import (fused_gate_add, fused_gate_add_layer_norm,
+                          fused_gate_add_ln_modulate_quant, fused_ln_modulate,
                           fused_ln_modulate_quant, layer_norm)
 from .cross_attn import unit_gate
 from .fp8_ffn import FP8FFN, gemm_gelu_quant_fp8
@@ -396,15 +397,21 @@ def _make_dit_block_forward(dit):
                 kv_len=kv_len, is_full_block=is_full_block, is_stream=is_stream,
                 pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v, local_range=local_range)
 
-        if fa is not None:
-            x = gate_add(x, gate_msa, self_attn_output)
-        else:
-            x = self.gate(x, gate_msa, self_attn_output)
         ln3 = _affine_layer_norm(self.norm3) if fa is not None else None
-        if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda:
-            normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2])
+        if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda and \
+                self_attn_output.is_contiguous() and gate_msa.is_contiguous():
+            # the gated residual and norm3 in one pass over the rows
+            x, normed = fused_gate_add_layer_norm(x, gate_msa, self_attn_output, ln3[0], ln3[1],
+                                                  eps=ln3[2])
         else:
-            normed = self.norm3(x)
+            if fa is not None:
+                x = gate_add(x, gate_msa, self_attn_output)
+            else:
+                x = self.gate(x, gate_msa, self_attn_output)
+            if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda:
+                normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2])
+            else:
+                normed = self.norm3(x)
         yc = self.cross_attn(normed, context, is_stream=is_stream)
         if rows and isinstance(self.ffn, FP8FFN) and yc.shape == x.shape and yc.is_contiguous():
             # x + cross-attention output and the FFN's AdaLN in one pass (a

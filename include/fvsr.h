@@ -154,6 +154,20 @@ int fvsr_gate_add_ln_modulate(const void* x, const void* gate, const void* res, 
 int fvsr_layer_norm(const void* x, const void* weight, const void* bias, void* out, int64_t rows,
                     int64_t D, float eps, void* codes, float* row_scale, void* stream);
 
+/*
+ * The self-attention's gated residual followed by norm3, one pass over the
+ * rows (integrate.py:151-171: x = fused_gate_add(x, gate_msa, attn_out);
+ * norm3(x)): x1 = bf16(x + bf16(gate * res)) written to x1 [B, L, D], then
+ * the affine LayerNorm of x1 as fvsr_layer_norm into out (and/or codes +
+ * row_scale).  gate bf16 [B, 1, D]; x, res, x1, out bf16 [B, L, D].  Same
+ * results as fvsr_gate_add followed by fvsr_layer_norm; vector path only
+ * (D % 8 == 0, D <= 1536, 16-byte aligned), else FVSR_EUNSUPPORTED.
+ */
+int fvsr_gate_add_layer_norm(const void* x, const void* gate, const void* res, void* x1,
+                             const void* weight, const void* bias, void* out, int64_t B,
+                             int64_t L, int64_t D, float eps, void* codes, float* row_scale,
+                             void* stream);
+
 /* out = bf16(x + bf16(gate*res)), reference fused_gate_add
  * (fused_adaln.py:45-57,74-85): x, res, out bf16 [B,L,D]; gate bf16 [B,1,D]. */
 int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out, int64_t B,

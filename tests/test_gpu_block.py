@@ -157,6 +157,24 @@ def test_dit_block_vs_oracle(cross_len):
     _close(host_f(y)[0], ref)
 
 
+@pytest.mark.parametrize("B,L,D", [(1, 4224, 1536), (2, 33, 1536), (1, 7, 512), (3, 5, 768)])
+def test_gate_add_layer_norm_fused_equals_separate(B, L, D):
+    """The self-attention's gated residual + norm3 in one pass is
+    bit-identical to fused_gate_add followed by the affine layer_norm; odd
+    row counts put a batch boundary inside a wavefront's row pair."""
+    import flashvsr_sm89_ops as fv
+    from flashvsr_sm89_ops.fused_adaln import fused_gate_add_layer_norm, layer_norm
+    g = torch.Generator().manual_seed(3 * B * L + D)
+    x, r = (torch.randn(B, L, D, generator=g).bfloat16().to(DEV) for _ in range(2))
+    gate = (0.3 * torch.randn(B, 1, D, generator=g)).bfloat16().to(DEV)
+    w = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(DEV)
+    b = (0.1 * torch.randn(D, generator=g)).bfloat16().to(DEV)
+    x1, y = fused_gate_add_layer_norm(x, gate, r, w, b, eps=1e-6)
+    x1r = fv.fused_gate_add(x, gate, r)
+    yr = layer_norm(x1r, w, b, eps=1e-6)
+    assert torch.equal(x1, x1r) and torch.equal(y, yr)
+
+
 @pytest.mark.parametrize("B,L,D", [(1, 4224, 1536), (2, 33, 1536), (1, 7, 512)])
 def test_gate_add_ln_modulate_fused_equals_separate(B, L, D):
     """The fused pass is bit-identical to fused_gate_add followed by
