@@ -94,6 +94,8 @@ def _window_maps(f, h, w, n_cache_rows, device):
         inv[tok.long()] = torch.arange(tok.numel(), dtype=torch.int32, device=device)
         kv_rows = (inv + n_cache_rows).contiguous()
         kv_map = torch.arange(n_cache_rows + tok.numel(), dtype=torch.int32, device=device)
+        if len(_MAPS) >= 32:  # a few geometries per run; keep the cache bounded
+            _MAPS.pop(next(iter(_MAPS)))
         m = _MAPS[key] = (tok, kv_rows, kv_map)
     return m
 
