@@ -299,3 +299,27 @@ def test_fused_block_equals_reference_dataflow(monkeypatch, per_token):
         assert torch.isfinite(y0.float()).all()
         assert torch.equal(k0, k1) and torch.equal(v0, v1)
         assert torch.equal(y0, y1)
+
+
+def test_qkv_rows_kernel_batch2_strided():
+    """Two batch elements and q/k/v as column slices of one [B, L, 3D] tensor
+    (the fused projection's output): RoPE position is the row within its
+    batch element, k and v rows land where kv_rows sends them."""
+    from flashvsr_sm89_ops.fused_rms_rope import fused_rms_rope_qk, fused_rms_rope_qkv_rows
+    dev = "cuda"
+    B, L = 2, 384
+    g = torch.Generator().manual_seed(21)
+    qkv = torch.randn(B, L, 3 * D, generator=g).to(torch.bfloat16).to(dev)
+    q, k, v = (qkv[..., i * D:(i + 1) * D] for i in range(3))
+    wq, wk = ((1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev) for _ in range(2))
+    fr = _freqs(L, dev)
+    rq, rk = fused_rms_rope_qk(q.contiguous(), k.contiguous(), wq, wk, fr, eps=1e-6, head_dim=HD)
+    perm = torch.randperm(B * L, generator=g).to(torch.int32).to(dev)
+    kbuf = torch.zeros((B * L, D), dtype=torch.bfloat16, device=dev)
+    vbuf = torch.zeros_like(kbuf)
+    vref = v.contiguous().reshape(B * L, D)
+    fused_rms_rope_qkv_rows(q, k, v, wq, wk, fr, kbuf, vbuf, perm, eps=1e-6, head_dim=HD)
+    torch.cuda.synchronize()
+    assert torch.equal(q, rq)  # rotated in place inside the fused tensor
+    assert torch.equal(kbuf[perm.long()], rk.reshape(B * L, D))
+    assert torch.equal(vbuf[perm.long()], vref)
