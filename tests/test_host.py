@@ -411,3 +411,38 @@ def test_window_path_shape_guard():
     assert not _window_path_ok(T((1, 2 * 12 * 24, 256)), 2, 12, 24, 128)  # h % 8
     assert not _window_path_ok(T((1, 768, 256)), 2, 16, 24, 64)            # head_dim
     assert not _window_path_ok(T((1, 768, 3072)), 2, 16, 24, 128)          # D > 1536
+
+
+def test_kv_store_appends_in_place_and_copies_foreign_caches():
+    """The copy-free self-attention's K/V store (integrate._kv_buffers), on
+    CPU tensors: the cache it returns, passed back unchanged, gets the next
+    chunk appended behind it in the same storage; a cache from elsewhere, or
+    a full store, is copied into a new store once."""
+    from flashvsr_sm89_ops.integrate import _kv_buffers
+    D, L = 8, 4
+    mod = types.SimpleNamespace(_fs89_kv=None)
+    like = torch.empty(0, dtype=torch.bfloat16)
+    kb, vb = _kv_buffers(mod, None, None, 0, L, D, like, True)   # first chunk
+    assert kb.shape == (L, D) and mod._fs89_kv[0].shape[0] == L + 4 * L
+    kb.copy_(torch.arange(L * D).view(L, D))
+    vb.copy_(-torch.arange(L * D).view(L, D))
+    ck, cv = kb[2:], vb[2:]                                       # the cache handed out
+    k2, v2 = _kv_buffers(mod, ck, cv, 2, L, D, like, True)       # appended in place
+    assert k2.untyped_storage().data_ptr() == kb.untyped_storage().data_ptr()
+    assert torch.equal(k2[:2], ck) and torch.equal(v2[:2], cv) and k2.shape == (2 + L, D)
+    foreign = ck.clone()
+    k3, v3 = _kv_buffers(mod, foreign, cv.clone(), 2, L, D, like, True)
+    assert k3.untyped_storage().data_ptr() != kb.untyped_storage().data_ptr()
+    assert torch.equal(k3[:2], foreign)
+    # fill the new store: 2 cached + 5 chunks of L fit in 2 + L + 4L rows; the next one does not
+    ck, cv = k3[-2:], v3[-2:]
+    base = k3.untyped_storage().data_ptr()
+    for step in range(4):
+        kk, vv = _kv_buffers(mod, ck, cv, 2, L, D, like, True)
+        assert kk.untyped_storage().data_ptr() == base
+        ck, cv = kk[-2:], vv[-2:]
+    kk, vv = _kv_buffers(mod, ck, cv, 2, L, D, like, True)
+    assert kk.untyped_storage().data_ptr() != base and torch.equal(kk[:2], ck)
+    # outside a stream no room is kept and nothing is remembered
+    kb, _ = _kv_buffers(mod, None, None, 0, L, D, like, False)
+    assert mod._fs89_kv is None and kb.untyped_storage().nbytes() == L * D * 2
