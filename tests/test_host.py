@@ -446,3 +446,37 @@ def test_kv_store_appends_in_place_and_copies_foreign_caches():
     # outside a stream no room is kept and nothing is remembered
     kb, _ = _kv_buffers(mod, None, None, 0, L, D, like, False)
     assert mod._fs89_kv is None and kb.untyped_storage().nbytes() == L * D * 2
+
+
+def test_qkv_fusion_weight_assembly():
+    """integrate._qkv_fused: one [3N, K] weight for the q/k/v FP8Linears,
+    per-tensor scales expanded to per-column vectors of the same value,
+    biases concatenated; rebuilt when a weight changes in place; refused
+    when the three cannot share one GEMM (mixed activation granularity or
+    bias presence, a non-FP8 projection)."""
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    from flashvsr_sm89_ops.integrate import _qkv_fused
+    g = torch.Generator().manual_seed(0)
+
+    def lin(scale, bias=True, per_token=False):
+        w8 = torch.randint(0, 120, (4, 8), generator=g, dtype=torch.uint8)
+        b = torch.randn(4, generator=g).to(torch.bfloat16) if bias else None
+        return FP8Linear.from_quantized(w8, scale, b, per_token=per_token)
+
+    mod = types.SimpleNamespace(q=lin(torch.tensor(0.5)), k=lin(torch.tensor(0.25)),
+                                v=lin(torch.tensor([1.0, 2.0, 3.0, 4.0])))
+    w3, s3, b3, per_token = _qkv_fused(mod)
+    assert w3.shape == (12, 8) and not per_token
+    assert torch.equal(w3.view(torch.uint8), torch.cat([mod.q.weight, mod.k.weight,
+                                                          mod.v.weight]).view(torch.uint8))
+    assert torch.equal(s3, torch.tensor([0.5] * 4 + [0.25] * 4 + [1.0, 2.0, 3.0, 4.0]))
+    assert torch.equal(b3, torch.cat([mod.q.bias, mod.k.bias, mod.v.bias]))
+    assert _qkv_fused(mod)[0] is w3                       # cached
+    with torch.no_grad():
+        mod.k.weight.view(torch.uint8).zero_()            # in-place change: rebuilt
+    assert not torch.equal(_qkv_fused(mod)[0].view(torch.uint8), w3.view(torch.uint8))
+    assert _qkv_fused(types.SimpleNamespace(q=mod.q, k=mod.k, v=lin(torch.tensor(1.0),
+                                                                   per_token=True))) is None
+    assert _qkv_fused(types.SimpleNamespace(q=mod.q, k=mod.k, v=lin(torch.tensor(1.0),
+                                                                   bias=False))) is None
+    assert _qkv_fused(types.SimpleNamespace(q=mod.q, k=mod.k, v=torch.nn.Linear(8, 4))) is None
