@@ -50,7 +50,7 @@ from .fp8_ffn import FP8FFN, gemm_gelu_quant_fp8
 from .block import window_token_map
 from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qkv_rows
 from .lcsa.draft import draft_index
-from .lcsa.hip_lcsa import block_sparse_attention_strided
+from .lcsa.hip_lcsa import block_sparse_attention_strided, build_csr
 
 
 def _FLAG(name, default):
@@ -167,7 +167,8 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
     the RMSNorm/RoPE pass directly in window order, behind the cached windows,
     in the K/V buffer (no partition, no torch.cat; see _kv_buffers); the
     attention writes its output in raster order (no reverse).  The draft mask
-    is the device one, reading q through the map.  Returns what the reference
+    is the device one reading q through the map (FS89_DRAFT=1), or the DiT's
+    own on a gathered window-ordered q.  Returns what the reference
     returns, the caches included (window-ordered [windows, 128, D] views)."""
     B, L, D = x.shape
     fq = _qkv_fused(self)
@@ -208,8 +209,16 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
         self.local_range = local_range
     nq = L // block_s
     q2 = q.reshape(L, D)  # a view (rows may be strided: column slice of the fused qkv)
-    index = draft_index(q2, k_w, nheads=self.num_heads, q_temporal=seqlen,
-                        local=self.local_attn_mask, topk=topk, nq=nq, q_map=tok)
+    if _FLAG("FS89_DRAFT", "0"):
+        index = draft_index(q2, k_w, nheads=self.num_heads, q_temporal=seqlen,
+                            local=self.local_attn_mask, topk=topk, nq=nq, q_map=tok)
+    else:
+        # The DiT's own draft mask (the reference's call, integrate.py:103-104)
+        # on window-ordered q (one gather) and the window-ordered K buffer.
+        q_w = q2.index_select(0, tok.long()).view(-1, block_s, D)
+        mask = dit.generate_draft_block_mask(B, self.num_heads, seqlen, q_w, k_w, topk=topk,
+                                             local_attn_mask=self.local_attn_mask)
+        index = build_csr(mask[0] if mask.dim() == 4 else mask)
     out = torch.empty((L, D), dtype=q.dtype, device=q.device)
     hd = self.head_dim
     block_sparse_attention_strided(

@@ -113,8 +113,8 @@ def _freqs(L, device):
     return torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
 
 
-@pytest.mark.parametrize("hw", [(16, 16), (16, 24)])
-def test_window_path_equals_copy_path(monkeypatch, hw):
+@pytest.mark.parametrize("hw,draft", [((16, 16), "1"), ((16, 24), "1"), ((16, 24), "0")])
+def test_window_path_equals_copy_path(monkeypatch, hw, draft):
     import flashvsr_sm89_ops as fv
     from flashvsr_sm89_ops import integrate
     h, w = hw
@@ -128,7 +128,9 @@ def test_window_path_equals_copy_path(monkeypatch, hw):
     dev = "cuda"
     dit = _fake_dit()
     monkeypatch.setenv("FS89_FP8", "")
-    monkeypatch.setenv("FS89_DRAFT", "1")
+    # "0": the DiT's own draft function (here the same restatement, called on
+    # window-ordered q and k) instead of the device draft through the map
+    monkeypatch.setenv("FS89_DRAFT", draft)
     fv.enable(_Pipe(), dit_module=dit, verbose=False)
     g = torch.Generator().manual_seed(5)
     attn = dit.SelfAttention(g).to(dev)

@@ -440,9 +440,12 @@ def test_kv_store_appends_in_place_and_copies_foreign_caches():
     for step in range(4):
         kk, vv = _kv_buffers(mod, ck, cv, 2, L, D, like, True)
         assert kk.untyped_storage().data_ptr() == base
+        kk[2:].fill_(step)  # the new chunk's rows (the kernel would write them)
+        vv[2:].fill_(-step)
         ck, cv = kk[-2:], vv[-2:]
     kk, vv = _kv_buffers(mod, ck, cv, 2, L, D, like, True)
     assert kk.untyped_storage().data_ptr() != base and torch.equal(kk[:2], ck)
+    assert torch.equal(vv[:2], cv)
     # outside a stream no room is kept and nothing is remembered
     kb, _ = _kv_buffers(mod, None, None, 0, L, D, like, False)
     assert mod._fs89_kv is None and kb.untyped_storage().nbytes() == L * D * 2
