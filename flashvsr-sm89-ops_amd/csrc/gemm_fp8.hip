@@ -72,8 +72,16 @@ FVSR_DEV void map_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
   const int first_m = group * kGroupM;
   const int gsize = min(tiles_m - first_m, kGroupM);
   const int in_group = logical % per_group;
-  tm = first_m + in_group % gsize;
-  tn = in_group / gsize;
+  if (tiles_n <= 8) {
+    // Narrow N (the 1536-wide projections: 6 column tiles): the column tiles
+    // of one row panel run side by side, so the panel (K = 8960 for ffn2) is
+    // fetched once per round (ffn2 232 -> 228 us, o 56.5 -> 55.6 us).
+    tm = first_m + in_group / tiles_n;
+    tn = in_group % tiles_n;
+  } else {
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+  }
 }
 
 FVSR_DEV void zero_acc(v16f (&acc)[4][4]) {
