@@ -157,6 +157,92 @@ FVSR_DEV void gelu_quant_row(u32x4_t (&v)[VPL], const uint16_t* tab, int64_t row
   if (lane == 0) scale_out[row] = amax / 448.0f;
 }
 
+// Codes of one row's GELU values against a given scale (the per-tensor
+// requantisation): lookup in place, then the same conversion and stores as
+// gelu_quant_row.
+template <int VPL>
+FVSR_DEV void gelu_codes_row(u32x4_t (&v)[VPL], const uint16_t* tab, int64_t row, int64_t cols,
+                             int nchunk, float r, float sc, uint8_t* codes) {
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[j][i] = (uint32_t)tab[v[j][i] & 0xffffu] | ((uint32_t)tab[v[j][i] >> 16] << 16);
+  const int lane = lane_here();
+  uint8_t* qr = codes + row * cols;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    // Packed values only: the unpacked lookups are not kept for this loop.
+    asm volatile("" : "+v"(v[j]));
+    const u32x2_t q = chunk_codes_fma(v[j], r, sc);
+    const int c = min(lane + 64 * j, nchunk - 1);
+    __builtin_nontemporal_store(q, (u32x2_t*)(qr + (uint32_t)c * 8u));
+  }
+}
+
+// Per-tensor GELU requantisation by table: the tensor's amax comes from
+// per-block partial maxima of |GELU| (every wave reduces them all: at most
+// 1024 floats), then rows as in quant_rows_gelu_table.  Same codes and scale
+// as quant_tensor<true, true>, whose GELU is evaluated per element.
+template <int VPL>
+__global__ __launch_bounds__(kTabWaves * 64) void quant_tensor_gelu_table(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    const float* __restrict__ part, int nparts, uint8_t* __restrict__ codes,
+    float* __restrict__ scale_out) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+  for (int i = threadIdx.x; i < 65536 / 8; i += kTabWaves * 64)
+    ((u32x4_t*)tab)[i] = ((const u32x4_t*)kGeluTable)[i];
+  const int lane = threadIdx.x & 63;
+  float m = 0.0f;
+  for (int i = lane; i < nparts; i += 64) m = fmaxf(m, part[i]);
+  const float amax = wave_max_abs(m);
+  __syncthreads();
+  const float s = qscale(amax), r = 1.0f / s, sc = qscale_fin(s);
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = amax / 448.0f;
+  const int nchunk = (int)(cols >> 3);
+  const int64_t stride = (int64_t)gridDim.x * kTabWaves;
+  u32x4_t v[VPL];
+  for (int64_t row = (int64_t)blockIdx.x * kTabWaves + (threadIdx.x >> 6); row < rows;
+       row += stride) {
+    load_row(v, x, row, ld, nchunk);
+    gelu_codes_row<VPL>(v, tab, row, cols, nchunk, r, sc, codes);
+  }
+}
+
+// Per-workgroup maxima of |GELU(x)| by table (the amax pass of the two-pass
+// per-tensor requantisation): part[blockIdx.x] for a persistent grid.
+template <int VPL>
+__global__ __launch_bounds__(kTabWaves * 64) void amax_gelu_table(
+    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    float* __restrict__ part) {
+  __shared__ __attribute__((aligned(16))) uint16_t tab[65536];
+  __shared__ float red[kTabWaves];
+  for (int i = threadIdx.x; i < 65536 / 8; i += kTabWaves * 64)
+    ((u32x4_t*)tab)[i] = ((const u32x4_t*)kGeluTable)[i];
+  __syncthreads();
+  const int nchunk = (int)(cols >> 3);
+  const int64_t stride = (int64_t)gridDim.x * kTabWaves;
+  float m = 0.0f;
+  u32x4_t v[VPL];
+  for (int64_t row = (int64_t)blockIdx.x * kTabWaves + (threadIdx.x >> 6); row < rows;
+       row += stride) {
+    load_row(v, x, row, ld, nchunk);  // a repeated chunk changes no maximum
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        m = max3_abs(m, bf2f(tab[v[j][i] & 0xffffu]), bf2f(tab[v[j][i] >> 16]));
+  }
+  m = wave_max_abs(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = 0.0f;
+    for (int w = 0; w < kTabWaves; ++w) b = fmaxf(b, red[w]);
+    part[blockIdx.x] = b;
+  }
+}
+
 template <int VPL>
 __global__ __launch_bounds__(kTabWaves * 64) void quant_rows_gelu_table(
     const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
@@ -399,12 +485,39 @@ int launch_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8
   return fvsr_launch_status();
 }
 
+// The per-tensor GELU quant pass: by table when rows fit 18 chunks per lane.
+void launch_gelu_tensor_codes(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
+                              const float* part, int P, uint8_t* q, float* s, hipStream_t st) {
+  if ((cols / 8 + 63) / 64 <= 18) {
+    const int64_t want = (rows + kTabWaves - 1) / kTabWaves;
+    const int64_t g = want < cu_count() ? want : cu_count();
+    hipLaunchKernelGGL((quant_tensor_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0,
+                       st, x, rows, cols, ld, part, P, q, s);
+  } else {
+    hipLaunchKernelGGL((quant_tensor<true, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
+                       ld, part, P, q, s);
+  }
+}
+
 template <bool GELU>
 int launch_tensor(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8_t* q,
                   float* s, float* ws, hipStream_t st) {
   const int P = partial_blocks(rows);
   const bool vec = (cols % 8 == 0) && (ld % 8 == 0) && aligned16(x) && aligned16(q);
-  if (vec) {
+  if (vec && GELU && (cols / 8 + 63) / 64 <= 18) {
+    // both passes by table; the grid is persistent, one partial per workgroup
+    const int64_t want = (rows + kTabWaves - 1) / kTabWaves;
+    int64_t g = want < cu_count() ? want : cu_count();
+    g = g < P ? g : P;
+    hipLaunchKernelGGL((amax_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0, st, x,
+                       rows, cols, ld, ws);
+    hipLaunchKernelGGL((quant_tensor_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0,
+                       st, x, rows, cols, ld, ws, (int)g, q, s);
+  } else if (vec && GELU) {
+    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
+                       ld, ws);
+    launch_gelu_tensor_codes(x, rows, cols, ld, ws, P, q, s, st);
+  } else if (vec) {
     hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
                        ld, ws);
     hipLaunchKernelGGL((quant_tensor<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
@@ -464,8 +577,7 @@ extern "C" int fvsr_gelu_quant_fp8_tensor(const void* h, int64_t rows, int64_t c
                      P, gpart);
   const bool vec = (cols % 8 == 0) && aligned16(h) && aligned16(codes);
   if (vec)
-    hipLaunchKernelGGL((quant_tensor<true, true>), dim3(P), dim3(kThreads), 0, st, hp, rows, cols,
-                       cols, gpart, P, qp, scale_out);
+    launch_gelu_tensor_codes(hp, rows, cols, cols, gpart, P, qp, scale_out, st);
   else
     hipLaunchKernelGGL((quant_tensor<true, false>), dim3(P), dim3(kThreads), 0, st, hp, rows,
                        cols, cols, gpart, P, qp, scale_out);

@@ -120,11 +120,11 @@ def _rows_of(vals, cols, head):
 
 
 def test_e4m3_fast_division_register_rows(ops):
-    """The register-resident row kernels multiply by 1/s and fall back to the
-    IEEE division near e4m3 rounding boundaries.  (a) Every finite bf16 value
-    with |v| <= 448, rows pinned at amax 448 (s = 1: every e4m3 midpoint that
-    bf16 can hold is hit exactly).  (b) e4m3 midpoints scaled by an inexact
-    s = 3/448 and their bf16 neighbours, so x*(1/s) and x/s can straddle."""
+    """The register-resident row kernels form x/s without dividing (one
+    product and two fmas, quot_abs).  (a) Every finite bf16 value with
+    |v| <= 448, rows pinned at amax 448 (s = 1: every e4m3 midpoint that bf16
+    can hold is hit exactly).  (b) e4m3 midpoints scaled by an inexact
+    s = 3/448 and their bf16 neighbours, where x*(1/s) alone would straddle."""
     b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     f = O.from_bf16_bits(b)
     keep = np.isfinite(f) & (np.abs(f) <= 448)
@@ -146,17 +146,19 @@ def test_e4m3_fast_division_register_rows(ops):
     assert np.array_equal(host_codes(q), rq) and np.array_equal(host_f(s).reshape(-1), rs)
 
 
-def test_gelu_quant_all_bf16_by_table(ops):
-    """Per-token GELU requantisation (table lookup in LDS) over every finite
-    bf16 pattern, rows grouped by magnitude so each row's scale keeps the
-    codes informative: codes and scales bit-exact with the oracle's GELU."""
+@pytest.mark.parametrize("per_token", [True, False])
+def test_gelu_quant_all_bf16_by_table(ops, per_token):
+    """GELU requantisation (table lookup in LDS) over every finite bf16
+    pattern, rows grouped by magnitude so each row's scale keeps the codes
+    informative (per token), or one scale for all (per tensor: both passes by
+    table): codes and scales bit-exact with the oracle's GELU."""
     b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     f = O.from_bf16_bits(b)
     fin = b[np.isfinite(f)]
     order = np.argsort(np.abs(O.from_bf16_bits(fin)), kind="stable")
     x = _rows_of(fin[order], 8960, np.zeros(0, np.uint16))
-    q, s = ops.fused_gelu_quant_fp8(dev_bf16(x), per_token=True)
-    rq, rs = O.quantize_fp8(x, per_row=True, gelu=True)
+    q, s = ops.fused_gelu_quant_fp8(dev_bf16(x), per_token=per_token)
+    rq, rs = O.quantize_fp8(x, per_row=per_token, gelu=True)
     assert np.array_equal(host_f(s).reshape(-1), rs)
     assert np.array_equal(host_codes(q), rq)
 
@@ -174,8 +176,8 @@ def test_gelu_quant_bitexact(ops, shape, per_token):
 @pytest.mark.parametrize("shape", [(4133, 8960), (4133, 1024)])
 def test_gelu_quant_rows_persistent(ops, shape):
     """More rows than the persistent table kernel has waves (256 workgroups of
-    8 on MI355X), so each wave loops over several rows and prefetches the next
-    one; about one row in ten takes the division fallback."""
+    11 on MI355X), so each wave loops over several rows; row lengths with and
+    without a partial last chunk per lane."""
     h = rnd_bits(shape, seed=7 + shape[1], scale=2.0)
     q, s = ops.fused_gelu_quant_fp8(dev_bf16(h), per_token=True)
     rq, rs = O.quantize_fp8(h, per_row=True, gelu=True)
