@@ -397,14 +397,16 @@ def components(torch, fv):
                             "attn_frac_bf16": fl_a / (t_a * 1e-3) / PEAK["bf16"],
                             "gemm_GFLOP": fl_g / 1e9, "attn_GFLOP": fl_a / 1e9}
     del xs
-    out["enable_block_step"] = enable_block_step(torch, fv, dev)
+    out["enable_block_step"] = enable_block_step(torch, fv, dev, per_token=True)
+    out["enable_block_step_per_tensor"] = enable_block_step(torch, fv, dev, per_token=False)
     return out
 
 
-def enable_block_step(torch, fv, dev):
+def enable_block_step(torch, fv, dev, per_token=True):
     """One DiT block through the forwards enable() installs, one streaming step
-    at the C5 geometry (f=2, 48x88 latent, cache of 2 time rows), per-token x
-    per-channel FP8 q/k/v/o and FFN, draft top-k 30%: the fused dataflow
+    at the C5 geometry (f=2, 48x88 latent, cache of 2 time rows), FP8 q/k/v/o
+    and FFN per token x per channel (or per tensor, the reference's default),
+    draft top-k 30%: the fused dataflow
     (FS89_WINDOW=1) against the reference's (FS89_WINDOW=0).  The
     cross-attention is a stand-in returning a fixed tensor (F3 is timed above)."""
     import types
@@ -424,7 +426,7 @@ def enable_block_step(torch, fv, dev):
         with torch.no_grad():
             m.weight.copy_(torch.randn(n, k, generator=g) * 0.02)
             m.bias.zero_()
-        return FP8Linear(m.to(dev), per_channel=True, per_token=True)
+        return FP8Linear(m.to(dev), per_channel=per_token, per_token=per_token)
 
     def part(x, win):
         B, f, h, w, C = x.shape
