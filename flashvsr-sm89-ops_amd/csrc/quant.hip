@@ -535,8 +535,7 @@ int launch_tensor(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uin
 
 extern "C" int64_t fvsr_quant_workspace_floats(int64_t rows, int64_t cols, int mode) {
   (void)cols;
-  (void)mode;
-  return partial_blocks(rows);
+  return mode == FVSR_SCALE_ROW ? 0 : partial_blocks(rows);
 }
 
 extern "C" int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mode,

@@ -22,7 +22,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .fp8_linear import FP8Linear, fp8_gemm
+from .fp8_linear import FP8Linear, fp8_gemm, quantize_input_fp8
 from .fp8_quant import FP8_MAX, _workspace, quantize_fp8  # noqa: F401
 
 
@@ -42,8 +42,9 @@ def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
     ws = _workspace(y2, M, K, mode)
     _lib.check(_lib.lib().fvsr_quant_fp8(y2.data_ptr(), M, K, y2.stride(0), mode, 1,
-                                         x8.data_ptr(), s.data_ptr(), ws.data_ptr(), ws.numel(),
-                                         _lib.stream(y2)), "fused_gelu_quant_fp8")
+                                         x8.data_ptr(), s.data_ptr(), _lib.ptr(ws),
+                                         0 if ws is None else ws.numel(), _lib.stream(y2)),
+               "fused_gelu_quant_fp8")
     return x8, s
 
 
@@ -81,28 +82,30 @@ class FP8FFN(nn.Module):
 
     def forward(self, x):
         shape = x.shape
-        x2 = x.reshape(-1, shape[-1])
         per_token = getattr(self.lin0, "per_token", False)
-        x8, s = quantize_fp8(x2, per_token=per_token)
+        x8, s = quantize_input_fp8(x.reshape(-1, shape[-1]), per_token)
         h8, hs = gemm_gelu_quant_fp8(x8, s, self.lin0, per_token)
         out = self.lin2._mm(h8, hs)
         return out.reshape(*shape[:-1], out.shape[-1])
 
 
+def _is_block_ffn(name: str) -> bool:
+    parts = name.split(".")
+    return len(parts) == 3 and parts[0] == "blocks" and parts[1].isdigit() and parts[2] == "ffn"
+
+
 def convert_ffn_fp8(model: nn.Module) -> int:
-    """Swap every `blocks.i.ffn` Sequential for FP8FFN; returns the count.
-    Requires convert_linears_fp8(model, parts=["ffn"]) first (fp8_ffn.py:99-115)."""
-    import re
-    pat = re.compile(r"^blocks\.\d+\.ffn$")
-    n = 0
-    for name, mod in list(model.named_modules()):
-        if not pat.match(name):
-            continue
-        l0, l2 = mod[0], mod[2]
-        assert type(l0).__name__ == "FP8Linear" and type(l2).__name__ == "FP8Linear", \
-            f"{name}: run convert_linears_fp8(parts=['ffn']) first"
-        parent_name, _, leaf = name.rpartition(".")
-        parent = model.get_submodule(parent_name)
-        setattr(parent, leaf, FP8FFN(l0, l2))
-        n += 1
-    return n
+    """Replace each DiT block's ``blocks.<i>.ffn`` = Sequential(Linear,
+    GELU(tanh), Linear) by FP8FFN over its two Linears; returns how many were
+    replaced (reference fp8_ffn.py:99-115).  The Linears must already be
+    FP8Linear (convert_linears_fp8 with the "ffn" part): otherwise
+    AssertionError, as in the reference.  FFNs already converted are left
+    alone, so a second call replaces nothing."""
+    found = [(name, mod) for name, mod in model.named_modules()
+             if _is_block_ffn(name) and not isinstance(mod, FP8FFN)]
+    for name, seq in found:
+        up, down = seq[0], seq[2]
+        assert isinstance(up, FP8Linear) and isinstance(down, FP8Linear), \
+            f"{name}: its Linears are not FP8 yet; run convert_linears_fp8(parts=['ffn']) first"
+        model.get_submodule(name.rpartition(".")[0]).ffn = FP8FFN(up, down)
+    return len(found)

@@ -12,6 +12,8 @@ Scale granularity is per tensor by default, as in the reference.
 """
 from __future__ import annotations
 
+import hashlib
+import json
 import re
 
 import torch
@@ -57,6 +59,54 @@ def fp8_gemm(x8: torch.Tensor, s: torch.Tensor, w8: torch.Tensor, w_scale: torch
     return out
 
 
+def quantize_input_fp8(x2: torch.Tensor, per_token: bool = False):
+    """Activation quantisation as FP8Linear.forward / FP8FFN.forward do it
+    (reference fp8_linear.py:35-40, fp8_ffn.py:88-92).  A contiguous [M, K]
+    goes through quantize_fp8.  For any other layout the reference evaluates
+    ``s = (x2.abs().amax() / 448).clamp(min=1e-12).float()`` and
+    ``(x2 / s).to(e4m3)`` eagerly: bf16 tensors, so the scale and x/s are
+    each rounded to bf16 before the cast.  That is the expression of its
+    per-tensor weight quantisation, so those codes come from the same kernel
+    (on a contiguous copy).  Per-token scales (this build's extension) read
+    strided rows directly."""
+    if per_token or x2.is_contiguous():
+        return quantize_fp8(x2, per_token=per_token)
+    _lib.require_gpu(x2)
+    _lib.require_dtype(x2, torch.bfloat16, "x2")
+    return quantize_weight_fp8(x2.contiguous(), per_channel=False)
+
+
+def source_fingerprint(weight: torch.Tensor, bias: torch.Tensor | None) -> str:
+    """Checksum of the weights an FP8Linear is quantised from (shape, dtype and
+    two wrapping int64 sums of the bit patterns, one position-weighted, for
+    the weight and the bias), computed where the tensors live.  A stored FP8
+    weight file records it per module so that codes are never applied to a
+    model whose source weights differ."""
+    parts = []
+    for t in (weight, bias):
+        if t is None:
+            parts.append(None)
+            continue
+        t = t.detach().contiguous().reshape(-1)
+        as_int = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[t.element_size()]
+        v = t.view(as_int).to(torch.int64)
+        pos = torch.arange(v.numel(), device=v.device, dtype=torch.int64)
+        mix = (pos * 0x9E3779B1 + 0x7F4A7C15) & 0xFFFFFFFF
+        parts.append((tuple(t.shape), str(t.dtype), int(v.sum()), int((v * mix).sum())))
+    parts.insert(0, tuple(weight.shape))
+    return hashlib.sha256(repr(parts).encode()).hexdigest()[:32]
+
+
+class StoredFP8Weights(dict):
+    """{module name: (codes uint8 [N, K], scales fp32, bias or None)} plus
+    ``fingerprints`` {module name: source_fingerprint of the weights the codes
+    were quantised from}."""
+
+    def __init__(self, *a, fingerprints=None, **k):
+        super().__init__(*a, **k)
+        self.fingerprints = dict(fingerprints or {})
+
+
 class FP8Linear(nn.Module):
     """Drop-in for the reference FP8Linear (fp8_linear.py:16-42)."""
 
@@ -68,7 +118,10 @@ class FP8Linear(nn.Module):
         if linear is None:  # filled by from_quantized
             return
         w = linear.weight.detach()
-        q, s = quantize_weight_fp8(w.to(torch.bfloat16), per_channel=per_channel)
+        if w.dtype != torch.bfloat16:
+            raise TypeError(f"FP8Linear quantises bf16 weights (the FlashVSR DiT's dtype); got "
+                            f"{w.dtype}. Cast the model to bfloat16 before converting.")
+        q, s = quantize_weight_fp8(w, per_channel=per_channel)
         bias = linear.bias.detach().clone() if linear.bias is not None else None
         self._set(q, s, bias)
 
@@ -103,8 +156,7 @@ class FP8Linear(nn.Module):
 
     def forward(self, x):
         shape = x.shape
-        x2 = x.reshape(-1, shape[-1])
-        x8, s = quantize_fp8(x2, per_token=self.per_token)
+        x8, s = quantize_input_fp8(x.reshape(-1, shape[-1]), self.per_token)
         y = self._mm(x8, s)
         return y.reshape(*shape[:-1], y.shape[-1])
 
@@ -121,7 +173,8 @@ def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_ch
     ("ffn" / "self" / "cross"); returns the number converted
     (fp8_linear.py:45-67).  Idempotent: FP8Linear is not an nn.Linear.
     ``stored`` (from load_fp8_weights) supplies saved codes and scales by
-    module name; those modules are not quantised again."""
+    module name; those modules are not quantised again, and when ``stored``
+    carries fingerprints each must match the module's current weights."""
     allowed = []
     if "self" in parts:
         allowed.append(r"^blocks\.\d+\.self_attn\.[qkvo]$")
@@ -136,6 +189,7 @@ def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_ch
             continue
         parent_name, _, leaf = name.rpartition(".")
         parent = model.get_submodule(parent_name) if parent_name else model
+        fp = source_fingerprint(mod.weight, mod.bias)
         if stored is not None and name in stored:
             w8, ws, b = stored[name]
             if tuple(w8.shape) != tuple(mod.weight.shape):
@@ -143,53 +197,66 @@ def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_ch
                                  f"the module {tuple(mod.weight.shape)}")
             if (ws.numel() == w8.shape[0] and w8.shape[0] != 1) != per_channel:
                 raise ValueError(f"stored FP8 weight for {name} has the other scale granularity")
+            want = getattr(stored, "fingerprints", {}).get(name)
+            if want is not None and want != fp:
+                raise ValueError(f"stored FP8 weight for {name} was quantised from different "
+                                 "weights than the module holds (source fingerprint mismatch); "
+                                 "delete the file to quantise again")
             dev = mod.weight.device
             new = FP8Linear.from_quantized(w8.to(dev), ws.to(dev),
                                            b.to(dev) if b is not None else None, per_token)
         else:
             new = FP8Linear(mod, per_channel=per_channel, per_token=per_token)
+        new.source_fingerprint = fp
         setattr(parent, leaf, new)
         n += 1
     return n
 
 
-FP8_WEIGHTS_FORMAT = "flashvsr-fp8-weights/1"
+FP8_WEIGHTS_FORMAT = "flashvsr-fp8-weights/2"
 
 
 def save_fp8_weights(model: nn.Module, path: str) -> int:
     """Persist every FP8Linear of ``model`` (codes as uint8 bit patterns, fp32
-    scales, bf16 biases) to a safetensors file; returns the number saved.
+    scales, bf16 biases, and in the metadata the fingerprint of the weights
+    each was quantised from) to a safetensors file; returns the number saved.
     Reloading gives bit-identical modules without quantising again."""
     from safetensors.torch import save_file
-    tensors = {}
-    n = 0
+    tensors, prints = {}, {}
     for name, mod in model.named_modules():
         if not isinstance(mod, FP8Linear):
             continue
+        fp = getattr(mod, "source_fingerprint", None)
+        if fp is None:
+            raise ValueError(f"{name}: FP8Linear without a source fingerprint (made outside "
+                             "convert_linears_fp8); cannot be saved as a weight file")
+        prints[name] = fp
         tensors[f"{name}.weight"] = mod.weight.detach().view(torch.uint8).contiguous().cpu()
         tensors[f"{name}.w_scale"] = mod.w_scale.detach().float().reshape(-1).contiguous().cpu()
         if mod.bias is not None:
             tensors[f"{name}.bias"] = mod.bias.detach().contiguous().cpu()
-        n += 1
-    save_file(tensors, path, metadata={"format": FP8_WEIGHTS_FORMAT})
-    return n
+    save_file(tensors, path, metadata={"format": FP8_WEIGHTS_FORMAT,
+                                       "fingerprints": json.dumps(prints, sort_keys=True)})
+    return len(prints)
 
 
-def load_fp8_weights(path: str) -> dict:
-    """{module name: (codes uint8 [N, K], scales fp32, bias or None)} from a
-    file written by save_fp8_weights (CPU tensors; nothing is executed from
-    the file)."""
+def load_fp8_weights(path: str) -> StoredFP8Weights:
+    """The contents of a file written by save_fp8_weights (CPU tensors;
+    nothing is executed from the file), with the source fingerprints that
+    convert_linears_fp8 checks against the model."""
     from safetensors import safe_open
-    out = {}
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
         if meta.get("format") != FP8_WEIGHTS_FORMAT:
             raise ValueError(f"{path}: not a {FP8_WEIGHTS_FORMAT} file")
+        out = StoredFP8Weights(fingerprints=json.loads(meta.get("fingerprints", "{}")))
         keys = set(f.keys())
         for k in sorted(keys):
             if not k.endswith(".weight"):
                 continue
             name = k[:-len(".weight")]
+            if name not in out.fingerprints:
+                raise ValueError(f"{path}: no source fingerprint for {name}")
             b = f.get_tensor(f"{name}.bias") if f"{name}.bias" in keys else None
             out[name] = (f.get_tensor(k), f.get_tensor(f"{name}.w_scale"), b)
     return out

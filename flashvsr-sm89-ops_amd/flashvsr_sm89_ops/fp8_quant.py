@@ -16,9 +16,10 @@ from . import _lib
 FP8_MAX = 448.0
 
 
-def _workspace(x: torch.Tensor, rows: int, cols: int, mode: int) -> torch.Tensor:
+def _workspace(x: torch.Tensor, rows: int, cols: int, mode: int):
+    """Per-tensor partial maxima (None for per-row scales, which need none)."""
     n = int(_lib.lib().fvsr_quant_workspace_floats(rows, cols, mode))
-    return torch.empty(max(n, 1), dtype=torch.float32, device=x.device)
+    return torch.empty(n, dtype=torch.float32, device=x.device) if n else None
 
 
 def quantize_fp8(x2: torch.Tensor, per_token: bool = False):
@@ -41,8 +42,9 @@ def quantize_fp8(x2: torch.Tensor, per_token: bool = False):
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
     ws = _workspace(x2, M, K, mode)
     _lib.check(_lib.lib().fvsr_quant_fp8(x2.data_ptr(), M, K, x2.stride(0), mode, 0,
-                                         q.data_ptr(), s.data_ptr(), ws.data_ptr(), ws.numel(),
-                                         _lib.stream(x2)), "quantize_fp8")
+                                         q.data_ptr(), s.data_ptr(), _lib.ptr(ws),
+                                         0 if ws is None else ws.numel(), _lib.stream(x2)),
+               "quantize_fp8")
     return q, s
 
 
@@ -59,6 +61,7 @@ def quantize_weight_fp8(w: torch.Tensor, per_channel: bool = False):
         mode = _lib.SCALE_ROW if per_channel else _lib.SCALE_TENSOR
         ws = _workspace(w, N, K, mode)
         _lib.check(_lib.lib().fvsr_quant_weight_fp8(w.data_ptr(), N, K, mode, q.data_ptr(),
-                                                    s.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                    s.data_ptr(), _lib.ptr(ws),
+                                                    0 if ws is None else ws.numel(),
                                                     _lib.stream(w)), "quantize_weight_fp8")
     return q, (s if per_channel else s.reshape(()))

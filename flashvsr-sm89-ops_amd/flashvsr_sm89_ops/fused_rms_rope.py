@@ -12,6 +12,8 @@ cached per freqs tensor.
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import _lib
@@ -21,18 +23,25 @@ _CS_CACHE_MAX = 8
 
 
 def _freqs_table(freqs: torch.Tensor) -> torch.Tensor:
-    """complex [..., S, head_dim/2] -> fp32 [S, head_dim/2, 2] contiguous (cos, sin)."""
+    """complex [..., S, head_dim/2] -> fp32 [S, head_dim/2, 2] contiguous (cos, sin).
+
+    A contiguous complex64 freqs is viewed without a copy.  Other dtypes (Wan
+    builds complex128) are converted once per freqs tensor: the entry holds a
+    weak reference to its source and is used only while that same tensor is
+    alive and unmodified (identity and version counter), so a new tensor that
+    reuses a freed one's address never gets the old table."""
     f = freqs.reshape(-1, freqs.shape[-1])
     if f.dtype == torch.complex64 and f.is_contiguous():
         return torch.view_as_real(f)
-    key = (freqs.data_ptr(), tuple(freqs.shape), freqs.dtype, freqs.device,
-           getattr(freqs, "_version", 0))
-    t = _CS_CACHE.get(key)
-    if t is None:
-        t = torch.view_as_real(f.to(torch.complex64)).contiguous()
-        if len(_CS_CACHE) >= _CS_CACHE_MAX:
-            _CS_CACHE.pop(next(iter(_CS_CACHE)))
-        _CS_CACHE[key] = t
+    entry = _CS_CACHE.get(id(freqs))
+    if entry is not None and entry[0]() is freqs and entry[1] == freqs._version:
+        return entry[2]
+    t = torch.view_as_real(f.to(torch.complex64)).contiguous()
+    for k in [k for k, e in _CS_CACHE.items() if e[0]() is None]:
+        del _CS_CACHE[k]                      # sources already freed
+    while len(_CS_CACHE) >= _CS_CACHE_MAX:
+        _CS_CACHE.pop(next(iter(_CS_CACHE)))
+    _CS_CACHE[id(freqs)] = (weakref.ref(freqs), freqs._version, t)
     return t
 
 

@@ -1,107 +1,168 @@
-"""One-call wiring of the operator pack into a FlashVSR v1.1 Tiny pipeline.
+"""Wiring of the operator pack into a FlashVSR v1.1 Tiny pipeline.
 
-``enable(pipe)`` keeps the reference's contract (flashvsr_sm89_ops/integrate.py:229-292):
-call it once after ``pipe.to('cuda')`` / ``pipe.enable_vram_management(...)``
-and before ``pipe.init_cross_kv()``.  In dependency order it
+``enable(pipe)`` honours the reference contract (flashvsr_sm89_ops/integrate.py:229-292):
+one call after ``pipe.to('cuda')`` / ``pipe.enable_vram_management(...)`` and
+before ``pipe.init_cross_kv()``, returning a dict of what it switched on, under
+the same ``FS89_*`` flags.  What it does, in order:
 
-1. sets the TCDecoder to channels_last (``FS89_TCDEC_CL``, default on);
-2. converts the DiT Linears to ``FP8Linear`` and the FFNs to ``FP8FFN``
-   (``FS89_FP8`` parts, ``FS89_FP8_FFNFUSED``), scale granularity from
-   ``FS89_FP8_SCALE`` = ``tensor`` (default, as the reference) or ``row``
-   (per-output-channel weights, per-token activations);
-3. rebinds upstream ``SelfAttention.forward`` / ``CrossAttention.forward`` /
-   ``DiTBlock.forward`` with fused-aware copies whose stock branches are the
-   upstream math, so each flag can be switched off (``FS89_FUSED_ROPE``,
-   ``FS89_FUSED_ADALN``);
-4. resolves ``block_sparse_attn`` to the HIP block-sparse attention;
-   ``FS89_DRAFT=1`` also computes the draft block mask on the device
-   (``lcsa/draft.py``, the bf16 reading of lcsa/reference.py:37-64) in place
-   of the DiT's ``generate_draft_block_mask`` (default off: the DiT's own
-   function is the one the reference calls);
-5. runs the cross-attention's dense attention over the cached prompt K/V on
-   the same HIP attention kernel with every block kept (``FS89_CROSS_ATTN``,
-   default on, shapes it covers: batch 1, head_dim 128, token counts in
-   multiples of 128; others keep the DiT's attention), and with
-   ``FS89_FUSED_ADALN`` the affine ``norm3`` LayerNorm before it.
+* decoder memory layout: the TCDecoder goes channels_last (``FS89_TCDEC_CL``);
+  ``FS89_TCDEC_COMPILE`` is accepted and reported but not applied (a
+  decoder-side inductor compile is not part of this pack and would bring
+  Triton back);
+* FP8 weights: the DiT block Linears become ``FP8Linear`` and the FFNs
+  ``FP8FFN`` (``FS89_FP8`` parts, ``FS89_FP8_FFNFUSED``), per tensor as the
+  reference or, with ``FS89_FP8_SCALE=row``, per output channel / per token;
+  ``FS89_FP8_WEIGHTS`` names a file of stored codes loaded instead of
+  quantising;
+* forwards: ``SelfAttention`` / ``CrossAttention`` / ``DiTBlock`` of the
+  upstream DiT module get forwards that run the HIP kernels.  The upstream
+  forwards are kept (captured before rebinding) and serve every call whose
+  fused flag is off (``FS89_FUSED_ROPE``, ``FS89_FUSED_ADALN``), so a flag
+  set to 0 gives the stock upstream computation;
+* attention: ``block_sparse_attn`` resolves to the HIP block-sparse kernel.
 
-Re-running ``enable`` on a patched pipeline is safe.  ``FS89_TCDEC_COMPILE``
-(torch.compile of the decoder MemBlocks) is accepted but not applied: it is a
-decoder-side inductor compile outside this operator pack, and inductor would
-bring Triton kernels back in.
+Beyond the reference: the self-attention runs without its layout copies when
+the shapes allow (``FS89_WINDOW``, default on), ``FS89_DRAFT=1`` computes the
+draft block mask on the device, and ``FS89_CROSS_ATTN`` (default on) runs the
+cross-attention's dense attention on the same HIP kernel.
+
+Calling ``enable`` again on a patched module refreshes the flags only.
 """
 from __future__ import annotations
 
+import collections
+import inspect
 import os
 import warnings
+import weakref
 
 import torch
 
+from .block import window_token_map
 from .compat_bsa import active_backend, ensure_bsa_available
-from .fp8_ffn import convert_ffn_fp8
+from .cross_attn import cross_attention, unit_gate
+from .cross_attn import supported as cross_supported
+from .fp8_ffn import FP8FFN, convert_ffn_fp8, gemm_gelu_quant_fp8
 from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm, load_fp8_weights, save_fp8_weights
 from .fp8_quant import quantize_fp8
-from .cross_attn import cross_attention
-from .cross_attn import supported as cross_supported
 from .fused_adaln import (fused_gate_add, fused_gate_add_layer_norm,
                           fused_gate_add_ln_modulate_quant, fused_ln_modulate,
                           fused_ln_modulate_quant, layer_norm)
-from .cross_attn import unit_gate
-from .fp8_ffn import FP8FFN, gemm_gelu_quant_fp8
-from .block import window_token_map
 from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qkv_rows
 from .lcsa.draft import draft_index
 from .lcsa.hip_lcsa import block_sparse_attention_strided, build_csr
 
+WINDOW = (2, 8, 8)              # frames x rows x columns of one attention window (128 tokens)
+_TOKENS_PER_WINDOW = WINDOW[0] * WINDOW[1] * WINDOW[2]
+_STOCK_ATTR = "_FS89_STOCK"     # the upstream forwards, captured before rebinding
 
-def _FLAG(name, default):
+# Arguments the rebound forwards pass on by name; an upstream class lacking one
+# of them is a revision this pack was not written against.
+_EXPECTED_SIGS = {
+    "SelfAttention": ("x", "freqs", "f", "h", "w", "local_num", "topk", "train_img",
+                      "block_id", "kv_len", "is_full_block", "is_stream",
+                      "pre_cache_k", "pre_cache_v", "local_range"),
+    "CrossAttention": ("x", "y", "is_stream"),
+    "DiTBlock": ("x", "context", "t_mod", "freqs", "f", "h", "w", "local_num", "topk",
+                 "train_img", "block_id", "kv_len", "is_full_block", "is_stream",
+                 "pre_cache_k", "pre_cache_v", "local_range"),
+}
+_UPSTREAM_HELPERS = ("WindowPartition3D", "generate_draft_block_mask")
+
+# The six modulation vectors, in the order the upstream DiT block splits
+# (modulation + t_mod) into (reference integrate.py:154-155).
+Modulation = collections.namedtuple(
+    "Modulation", "shift_msa scale_msa gate_msa shift_mlp scale_mlp gate_mlp")
+
+
+def _on(name: str, default: str = "1") -> bool:
     return os.environ.get(name, default) == "1"
 
 
-def _unwrap(m):
-    """enable_vram_management wraps norms/linears in AutoWrappedModule."""
+def _inner(m):
+    """The module behind an enable_vram_management wrapper (or m itself)."""
     return getattr(m, "module", m)
 
 
-def _module_eps(m, default=1e-6):
-    return getattr(_unwrap(m), "eps", default)
+def _eps(m, default=1e-6):
+    return getattr(_inner(m), "eps", default)
 
+
+# ----------------------------------------------------------------------------- geometry
 
 def _window_path_on() -> bool:
-    return _FLAG("FS89_WINDOW", "1") and active_backend() == "hip"
+    return _on("FS89_WINDOW") and active_backend() == "hip"
 
 
 def _window_path_ok(x, f, h, w, head_dim) -> bool:
-    """Shapes the copy-free path serves: batch 1, bf16 on the GPU, whole
-    2x8x8 windows, head_dim 128, a hidden size the fused kernels take."""
+    """Shapes the copy-free self-attention serves: batch 1, bf16 on the GPU,
+    whole windows, head_dim 128, a hidden size the fused kernels take."""
     B, L, D = x.shape
-    return (B == 1 and x.dtype == torch.bfloat16 and x.is_cuda and head_dim == 128
-            and f % 2 == 0 and h % 8 == 0 and w % 8 == 0 and L == f * h * w
-            and D % head_dim == 0 and D <= 1536)
+    whole = f % WINDOW[0] == 0 and h % WINDOW[1] == 0 and w % WINDOW[2] == 0
+    return (B == 1 and x.dtype == torch.bfloat16 and x.is_cuda and head_dim == 128 and whole
+            and L == f * h * w and D % head_dim == 0 and D <= 1536)
 
 
-_MAPS = {}
+def _check_stream_geometry(x, f, h, w, is_stream, pre_k, pre_v):
+    """The upstream self-attention's preconditions: a streaming run starts with
+    6 latent frames and continues 2 at a time; L is f*h*w."""
+    cached = pre_k is not None and pre_v is not None
+    if is_stream:
+        want = 2 if cached else 6
+        if f != want:
+            raise AssertionError(f"streaming self-attention expects f == {want} "
+                                 f"({'with' if cached else 'without'} a KV cache), got {f}")
+    if x.shape[1] != f * h * w:
+        raise AssertionError(f"sequence length {x.shape[1]} != f*h*w = {f}*{h}*{w}")
+
+
+_MAPS: dict = {}
 
 
 def _window_maps(f, h, w, n_cache_rows, device):
-    """(tok_map, kv_rows, kv_map) for one (f, h, w, cache) geometry: window
-    position -> raster token; raster token -> row of the K/V buffer (after the
-    cached rows); identity over the whole K/V buffer."""
+    """(tok, kv_rows, kv_map) for one geometry: tok[i] = raster token at window
+    position i; kv_rows[t] = row of raster token t in the K/V buffer (after the
+    cached rows); kv_map = identity over the whole K/V buffer."""
     key = (f, h, w, n_cache_rows, str(device))
-    m = _MAPS.get(key)
-    if m is None:
-        tok = window_token_map(f, h, w, device=device)
-        inv = torch.empty_like(tok)
-        inv[tok.long()] = torch.arange(tok.numel(), dtype=torch.int32, device=device)
-        kv_rows = (inv + n_cache_rows).contiguous()
-        kv_map = torch.arange(n_cache_rows + tok.numel(), dtype=torch.int32, device=device)
-        if len(_MAPS) >= 32:  # a few geometries per run; keep the cache bounded
-            _MAPS.pop(next(iter(_MAPS)))
-        m = _MAPS[key] = (tok, kv_rows, kv_map)
-    return m
+    hit = _MAPS.get(key)
+    if hit is not None:
+        return hit
+    tok = window_token_map(f, h, w, device=device)
+    pos = torch.empty_like(tok)
+    pos[tok.long()] = torch.arange(tok.numel(), dtype=torch.int32, device=device)
+    val = (tok, (pos + n_cache_rows).contiguous(),
+           torch.arange(n_cache_rows + tok.numel(), dtype=torch.int32, device=device))
+    while len(_MAPS) >= 32:          # a handful of geometries per run
+        _MAPS.pop(next(iter(_MAPS)))
+    _MAPS[key] = val
+    return val
 
+
+def _refresh_local_mask(dit, mod, h, w, local_range, device):
+    """The module's local window rule, rebuilt by the upstream builder when the
+    window grid or the range changes (state kept on the module as upstream does)."""
+    bh, bw = h // WINDOW[1], w // WINDOW[2]
+    stale = (mod.local_attn_mask is None or mod.local_attn_mask_h != bh
+             or mod.local_attn_mask_w != bw or mod.local_range != local_range)
+    if stale:
+        mod.local_attn_mask = dit.build_local_block_mask_shifted_vec_normal_slide(
+            bh, bw, local_range, local_range, include_self=True, device=device)
+        mod.local_attn_mask_h, mod.local_attn_mask_w = bh, bw
+        mod.local_range = local_range
+    return mod.local_attn_mask
+
+
+def _trim_cache(k_w, v_w, windows_per_step, kv_len):
+    """Drop the oldest step's windows once the cache holds more than kv_len steps."""
+    if k_w.shape[0] // windows_per_step > kv_len:
+        return k_w[windows_per_step:], v_w[windows_per_step:]
+    return k_w, v_w
+
+
+# ----------------------------------------------------------------------------- K/V store
 
 def _appendable(t, store, frontier):
-    """t is a contiguous row range of `store` that ends at row `frontier`."""
+    """t is a contiguous row range of `store` ending at row `frontier`."""
     D = store.shape[1]
     return (t.is_contiguous() and t.device == store.device and t.dtype == store.dtype
             and t.untyped_storage().data_ptr() == store.untyped_storage().data_ptr()
@@ -110,20 +171,20 @@ def _appendable(t, store, frontier):
 
 def _kv_buffers(mod, pre_k, pre_v, cache_rows, L, D, like, grow):
     """K/V buffers [cache_rows + L, D] whose first rows hold the cached windows.
-    The caches this path returns are views of a per-module store with room
-    after them; when the caller passes them back unchanged (the streaming
-    loop does), the new chunk is appended behind them in place and the cache
-    is not copied (the reference concatenates).  Otherwise, or when the store
-    is full, a new store is made and the cache copied into it once."""
-    st = getattr(mod, "_fs89_kv", None)
-    if st is not None and cache_rows and pre_k is not None and pre_v is not None:
-        sk, sv, fr = st
-        if fr + L <= sk.shape[0] and _appendable(pre_k, sk, fr) and _appendable(pre_v, sv, fr):
-            start = fr - cache_rows
-            mod._fs89_kv = (sk, sv, fr + L)
-            return sk[start:fr + L], sv[start:fr + L]
+
+    The caches handed back are views into a per-module store with spare rows
+    behind them.  When the caller passes them back unchanged (the streaming
+    loop does) the next chunk lands behind them in place; any other cache, or
+    a full store, is copied once into a fresh store."""
+    store = getattr(mod, "_fs89_kv", None)
+    if store is not None and cache_rows and pre_k is not None and pre_v is not None:
+        sk, sv, end = store
+        if end + L <= sk.shape[0] and _appendable(pre_k, sk, end) and _appendable(pre_v, sv, end):
+            mod._fs89_kv = (sk, sv, end + L)
+            first = end - cache_rows
+            return sk[first:end + L], sv[first:end + L]
     rows = cache_rows + L
-    cap = rows + (4 * L if grow else 0)  # room for a few appended chunks
+    cap = rows + 4 * L if grow else rows   # room for a few appended chunks
     sk = torch.empty((cap, D), dtype=like.dtype, device=like.device)
     sv = torch.empty((cap, D), dtype=like.dtype, device=like.device)
     if cache_rows:
@@ -133,429 +194,388 @@ def _kv_buffers(mod, pre_k, pre_v, cache_rows, L, D, like, grow):
     return sk[:rows], sv[:rows]
 
 
+# ----------------------------------------------------------------------------- fused q/k/v weight
+
+def _same_tensor(ref, t) -> bool:
+    if ref is None:
+        return t is None
+    obj, version = ref
+    return t is not None and obj() is t and version == t._version
+
+
+def _track(t):
+    return None if t is None else (weakref.ref(t), t._version)
+
+
 def _qkv_fused(mod):
-    """One [3D, D] e4m3 weight for the q, k and v FP8Linears (built once per
-    module, rebuilt if any of them changes): the three projections of the
-    same activations become one GEMM on one quantisation of them (the
-    reference quantises the input three times).  Per-tensor weight scales
-    become per-column vectors of the same value, which the GEMM epilogue
-    applies with the same arithmetic.  None when the three cannot share."""
+    """(w3, s3, b3, per_token): one [3D, D] e4m3 weight for the module's q, k
+    and v FP8Linears, so the three projections of the same activations are one
+    GEMM over one quantisation of them.  Per-tensor weight scales become
+    per-column vectors of the same value (the epilogue arithmetic is the same).
+    Built once per module and rebuilt when any of the nine source tensors is
+    replaced or changed in place (tracked by identity and version counter, so
+    a new tensor at a freed one's address is not mistaken for it).  None when
+    the three cannot share one GEMM."""
     lins = [getattr(mod, n, None) for n in ("q", "k", "v")]
     if not all(isinstance(l, FP8Linear) for l in lins):
         return None
-    if len({l.per_token for l in lins}) != 1 or len({l.in_features for l in lins}) != 1:
+    if len({(l.per_token, l.in_features, l.bias is None) for l in lins}) != 1:
         return None
-    if len({l.bias is None for l in lins}) != 1:
-        return None
-    key = tuple((l.weight.data_ptr(), l.weight._version, l.w_scale.data_ptr(), l.w_scale._version,
-                 None if l.bias is None else (l.bias.data_ptr(), l.bias._version)) for l in lins)
-    c = getattr(mod, "_fs89_qkv", None)
-    if c is not None and c[0] == key:
-        return c[1]
+    srcs = [t for l in lins for t in (l.weight, l.w_scale, l.bias)]
+    cached = getattr(mod, "_fs89_qkv", None)
+    if cached is not None and all(_same_tensor(r, t) for r, t in zip(cached[0], srcs)):
+        return cached[1]
     w3 = torch.cat([l.weight for l in lins]).contiguous()
-    s3 = torch.cat([l.w_scale.float().reshape(-1).expand(l.out_features) for l in lins]).contiguous()
+    s3 = torch.cat([l.w_scale.float().reshape(-1).expand(l.out_features) for l in lins])
     b3 = None if lins[0].bias is None else torch.cat([l.bias for l in lins]).contiguous()
-    val = (w3, s3, b3, lins[0].per_token)
-    mod._fs89_qkv = (key, val)
+    val = (w3, s3.contiguous(), b3, lins[0].per_token)
+    mod._fs89_qkv = ([_track(t) for t in srcs], val)
     return val
 
 
+# ----------------------------------------------------------------------------- self-attention
+
 def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream, pre_cache_k,
                            pre_cache_v, local_range, x8s=None):
-    """The self-attention of integrate.py:42-126 without its layout copies (F2):
-    q stays in raster order and is read through the window map; k and v leave
-    the RMSNorm/RoPE pass directly in window order, behind the cached windows,
-    in the K/V buffer (no partition, no torch.cat; see _kv_buffers); the
-    attention writes its output in raster order (no reverse).  The draft mask
-    is the device one reading q through the map (FS89_DRAFT=1), or the DiT's
-    own on a gathered window-ordered q.  Returns what the reference
-    returns, the caches included (window-ordered [windows, 128, D] views)."""
+    """Self-attention (reference integrate.py:47-124) without its layout
+    copies: q stays in raster order and is read through the window map; k and
+    v leave the RMSNorm/RoPE pass directly in window order behind the cached
+    windows of the K/V store; the attention writes its output rows back in
+    raster order.  The draft mask is the device one through the map
+    (FS89_DRAFT=1) or the DiT's own on a gathered window-ordered q.
+    ``x8s`` = (codes, scales) of x when the caller already quantised it.
+    Returns what the upstream forward returns, window-ordered caches
+    ([windows, 128, D] views of the store) included."""
     B, L, D = x.shape
-    fq = _qkv_fused(self)
-    if fq is not None:
-        w3, s3, b3, per_token = fq
+    fused = _qkv_fused(self)
+    if fused is not None:
+        w3, s3, b3, per_token = fused
         if x8s is None:
             x8s = quantize_fp8(x.reshape(-1, D), per_token=per_token)
-        qkv = fp8_gemm(x8s[0], x8s[1], w3, s3, b3)  # [L, 3D]: q, k, v column slices
+        qkv = fp8_gemm(x8s[0], x8s[1], w3, s3, b3)      # [L, 3D]: q | k | v columns
         q, k, v = (qkv[:, i * D:(i + 1) * D].view(B, L, D) for i in range(3))
+    elif x8s is not None:
+        raise ValueError("activation codes given but q/k/v are not FP8 linears")
     else:
-        if x8s is not None:
-            raise ValueError("activation codes given but q/k/v are not FP8 linears")
-        q = self.q(x).contiguous()
-        k = self.k(x).contiguous()
-        v = self.v(x).contiguous()
-    win = (2, 8, 8)
-    seqlen = f // win[0]
-    block_s = win[0] * win[1] * win[2]
-    one_len = L // block_s // seqlen
-    n_cache = 0 if pre_cache_k is None or pre_cache_v is None else pre_cache_k.shape[0]
-    kbuf, vbuf = _kv_buffers(self, pre_cache_k, pre_cache_v, n_cache * block_s, L, D, q,
-                             is_stream)
-    if _module_eps(self.norm_k) != _module_eps(self.norm_q):
+        q, k, v = (proj(x).contiguous() for proj in (self.q, self.k, self.v))
+    steps = f // WINDOW[0]
+    windows_per_step = L // _TOKENS_PER_WINDOW // steps
+    n_cached = 0 if pre_cache_k is None or pre_cache_v is None else pre_cache_k.shape[0]
+    cache_rows = n_cached * _TOKENS_PER_WINDOW
+    kbuf, vbuf = _kv_buffers(self, pre_cache_k, pre_cache_v, cache_rows, L, D, q, is_stream)
+    if _eps(self.norm_k) != _eps(self.norm_q):
         raise NotImplementedError("q and k RMSNorm eps differ")
-    tok, kv_rows, kv_map = _window_maps(f, h, w, n_cache * block_s, q.device)
-    fused_rms_rope_qkv_rows(q, k, v, _unwrap(self.norm_q).weight, _unwrap(self.norm_k).weight,
-                            freqs, kbuf, vbuf, kv_rows, eps=_module_eps(self.norm_q),
+    tok, kv_rows, kv_map = _window_maps(f, h, w, cache_rows, q.device)
+    fused_rms_rope_qkv_rows(q, k, v, _inner(self.norm_q).weight, _inner(self.norm_k).weight,
+                            freqs, kbuf, vbuf, kv_rows, eps=_eps(self.norm_q),
                             head_dim=self.head_dim)
-    k_w = kbuf.view(-1, block_s, D)
-    v_w = vbuf.view(-1, block_s, D)
-
-    if self.local_attn_mask is None or self.local_attn_mask_h != h // 8 \
-            or self.local_attn_mask_w != w // 8 or self.local_range != local_range:
-        self.local_attn_mask = dit.build_local_block_mask_shifted_vec_normal_slide(
-            h // 8, w // 8, local_range, local_range, include_self=True, device=k_w.device)
-        self.local_attn_mask_h = h // 8
-        self.local_attn_mask_w = w // 8
-        self.local_range = local_range
-    nq = L // block_s
-    q2 = q.reshape(L, D)  # a view (rows may be strided: column slice of the fused qkv)
-    if _FLAG("FS89_DRAFT", "0"):
-        index = draft_index(q2, k_w, nheads=self.num_heads, q_temporal=seqlen,
-                            local=self.local_attn_mask, topk=topk, nq=nq, q_map=tok)
+    k_w = kbuf.view(-1, _TOKENS_PER_WINDOW, D)
+    v_w = vbuf.view(-1, _TOKENS_PER_WINDOW, D)
+    local = _refresh_local_mask(dit, self, h, w, local_range, k_w.device)
+    q2 = q.reshape(L, D)            # rows may be strided (a column slice of qkv)
+    if _on("FS89_DRAFT", "0"):
+        index = draft_index(q2, k_w, nheads=self.num_heads, q_temporal=steps, local=local,
+                            topk=topk, nq=L // _TOKENS_PER_WINDOW, q_map=tok)
     else:
-        # The DiT's own draft mask (the reference's call, integrate.py:103-104)
-        # on window-ordered q (one gather) and the window-ordered K buffer.
-        q_w = q2.index_select(0, tok.long()).view(-1, block_s, D)
-        mask = dit.generate_draft_block_mask(B, self.num_heads, seqlen, q_w, k_w, topk=topk,
-                                             local_attn_mask=self.local_attn_mask)
+        q_w = q2.index_select(0, tok.long()).view(-1, _TOKENS_PER_WINDOW, D)
+        mask = dit.generate_draft_block_mask(B, self.num_heads, steps, q_w, k_w, topk=topk,
+                                             local_attn_mask=local)
         index = build_csr(mask[0] if mask.dim() == 4 else mask)
     out = torch.empty((L, D), dtype=q.dtype, device=q.device)
     hd = self.head_dim
     block_sparse_attention_strided(
         q2, kbuf, vbuf, None, None, heads=self.num_heads, head_dim=hd,
-        q_strides=(q2.stride(0), hd), kv_strides=(D, hd), out=out, o_strides=(D, hd), q_map=tok,
-        kv_map=kv_map, index=index)
-
-    cache_num = k_w.shape[0] // one_len
-    if cache_num > kv_len:
-        cache_k, cache_v = k_w[one_len:], v_w[one_len:]
-    else:
-        cache_k, cache_v = k_w, v_w
+        q_strides=(q2.stride(0), hd), kv_strides=(D, hd), out=out, o_strides=(D, hd),
+        q_map=tok, kv_map=kv_map, index=index)
+    cache_k, cache_v = _trim_cache(k_w, v_w, windows_per_step, kv_len)
     y = self.o(out.view(B, L, D))
-    if is_stream:
-        return y, cache_k, cache_v
-    return y
+    return (y, cache_k, cache_v) if is_stream else y
 
 
-def _make_self_attn_forward(dit):
-    """Fused-aware copy of upstream SelfAttention.forward (integrate.py:42-126);
-    with FUSED_ROPE_FN=None the stock branch reproduces upstream exactly."""
-    from einops import rearrange
+def _partitioned_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream,
+                                pre_cache_k, pre_cache_v, local_range):
+    """Self-attention with the fused RMSNorm+RoPE on materialised window
+    tensors, for shapes the copy-free path does not take: the upstream
+    partition / cache concatenation / reverse, the module's own attention."""
+    B, L, D = x.shape
+    rope = dit.FUSED_ROPE_FN
+    q = rope(self.q(x), _inner(self.norm_q).weight, freqs, eps=_eps(self.norm_q), rope=True,
+             head_dim=self.head_dim)
+    k = rope(self.k(x), _inner(self.norm_k).weight, freqs, eps=_eps(self.norm_k), rope=True,
+             head_dim=self.head_dim)
+    v = self.v(x)
+    grid = (B, f, h, w, D)
+    q_w, k_w, v_w = (dit.WindowPartition3D.partition(t.view(grid), WINDOW) for t in (q, k, v))
+    steps = f // WINDOW[0]
+    windows_per_step = k_w.shape[0] // B // steps
+    if pre_cache_k is not None and pre_cache_v is not None:
+        k_w = torch.cat([pre_cache_k, k_w], dim=0)
+        v_w = torch.cat([pre_cache_v, v_w], dim=0)
+    local = _refresh_local_mask(dit, self, h, w, local_range, k_w.device)
+    draft = dit.generate_draft_block_mask
+    if _on("FS89_DRAFT", "0"):
+        from .lcsa.draft import generate_draft_block_mask as draft
+    mask = draft(B, self.num_heads, steps, q_w, k_w, topk=topk, local_attn_mask=local)
+    # window-major token sequences per batch element, as the attention takes them
+    seq = [t.reshape(B, -1, D) for t in (q_w, k_w, v_w)]
+    out = self.attn(*seq, mask)
+    cache_k, cache_v = _trim_cache(k_w, v_w, windows_per_step, kv_len)
+    out = dit.WindowPartition3D.reverse(out.reshape(-1, q_w.shape[1], D), WINDOW, (f, h, w))
+    y = self.o(out.reshape(B, L, D))
+    return (y, cache_k, cache_v) if is_stream else y
 
+
+def _make_self_attn_forward(dit, stock):
     def forward(self, x, freqs, f=None, h=None, w=None, local_num=None, topk=None,
                 train_img=False, block_id=None, kv_len=None, is_full_block=False,
                 is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
-        B, L, D = x.shape
-        if is_stream and pre_cache_k is not None and pre_cache_v is not None:
-            assert f == 2, "f must be 2"
-        if is_stream and (pre_cache_k is None or pre_cache_v is None):
-            assert f == 6, " start f must be 6"
-        assert L == f * h * w, "Sequence length mismatch with provided (f,h,w)."
+        if getattr(dit, "FUSED_ROPE_FN", None) is None:
+            return stock(self, x, freqs, f=f, h=h, w=w, local_num=local_num, topk=topk,
+                         train_img=train_img, block_id=block_id, kv_len=kv_len,
+                         is_full_block=is_full_block, is_stream=is_stream,
+                         pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v,
+                         local_range=local_range)
+        _check_stream_geometry(x, f, h, w, is_stream, pre_cache_k, pre_cache_v)
+        path = (_window_self_attention
+                if _window_path_ok(x, f, h, w, self.head_dim) and _window_path_on()
+                else _partitioned_self_attention)
+        return path(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream, pre_cache_k,
+                    pre_cache_v, local_range)
 
-        rope_fn = getattr(dit, "FUSED_ROPE_FN", None)
-        if rope_fn is not None and _window_path_ok(x, f, h, w, self.head_dim) and _window_path_on():
-            return _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream,
-                                          pre_cache_k, pre_cache_v, local_range)
-        if rope_fn is not None:
-            q = rope_fn(self.q(x), _unwrap(self.norm_q).weight, freqs,
-                        eps=_module_eps(self.norm_q), rope=True, head_dim=self.head_dim)
-            k = rope_fn(self.k(x), _unwrap(self.norm_k).weight, freqs,
-                        eps=_module_eps(self.norm_k), rope=True, head_dim=self.head_dim)
-        else:
-            q = self.norm_q(self.q(x))
-            k = self.norm_k(self.k(x))
-            q = dit.rope_apply(q, freqs, self.num_heads)
-            k = dit.rope_apply(k, freqs, self.num_heads)
-        v = self.v(x)
-
-        win = (2, 8, 8)
-        q = q.view(B, f, h, w, D)
-        k = k.view(B, f, h, w, D)
-        v = v.view(B, f, h, w, D)
-
-        q_w = dit.WindowPartition3D.partition(q, win)
-        k_w = dit.WindowPartition3D.partition(k, win)
-        v_w = dit.WindowPartition3D.partition(v, win)
-
-        seqlen = f // win[0]
-        one_len = k_w.shape[0] // B // seqlen
-        if pre_cache_k is not None and pre_cache_v is not None:
-            k_w = torch.cat([pre_cache_k, k_w], dim=0)
-            v_w = torch.cat([pre_cache_v, v_w], dim=0)
-
-        block_n = q_w.shape[0] // B
-        block_s = q_w.shape[1]
-        block_n_kv = k_w.shape[0] // B
-
-        reorder_q = rearrange(q_w, '(b block_n) (block_s) d -> b (block_n block_s) d',
-                              block_n=block_n, block_s=block_s)
-        reorder_k = rearrange(k_w, '(b block_n) (block_s) d -> b (block_n block_s) d',
-                              block_n=block_n_kv, block_s=block_s)
-        reorder_v = rearrange(v_w, '(b block_n) (block_s) d -> b (block_n block_s) d',
-                              block_n=block_n_kv, block_s=block_s)
-
-        if self.local_attn_mask is None or self.local_attn_mask_h != h // 8 \
-                or self.local_attn_mask_w != w // 8 or self.local_range != local_range:
-            self.local_attn_mask = dit.build_local_block_mask_shifted_vec_normal_slide(
-                h // 8, w // 8, local_range, local_range, include_self=True, device=k_w.device)
-            self.local_attn_mask_h = h // 8
-            self.local_attn_mask_w = w // 8
-            self.local_range = local_range
-        draft = dit.generate_draft_block_mask
-        if _FLAG("FS89_DRAFT", "0"):
-            from .lcsa.draft import generate_draft_block_mask as draft
-        attention_mask = draft(
-            B, self.num_heads, seqlen, q_w, k_w, topk=topk, local_attn_mask=self.local_attn_mask)
-
-        x = self.attn(reorder_q, reorder_k, reorder_v, attention_mask)
-
-        cur_block_n, cur_block_s, _ = k_w.shape
-        cache_num = cur_block_n // one_len
-        if cache_num > kv_len:
-            cache_k = k_w[one_len:, :, :]
-            cache_v = v_w[one_len:, :, :]
-        else:
-            cache_k = k_w
-            cache_v = v_w
-
-        x = rearrange(x, 'b (block_n block_s) d -> (b block_n) (block_s) d',
-                      block_n=block_n, block_s=block_s)
-        x = dit.WindowPartition3D.reverse(x, win, (f, h, w))
-        x = x.view(B, f * h * w, D)
-
-        if is_stream:
-            return self.o(x), cache_k, cache_v
-        return self.o(x)
-
+    forward.__doc__ = ("SelfAttention.forward with fused RMSNorm+RoPE and the HIP attention "
+                       "(reference integrate.py:47-124); the upstream forward when "
+                       "FS89_FUSED_ROPE is off.")
     return forward
 
 
-def _make_cross_attn_forward(dit):
-    """Fused-aware copy of upstream CrossAttention.forward (integrate.py:129-145)."""
+# ----------------------------------------------------------------------------- cross-attention
 
+def _make_cross_attn_forward(dit, stock):
+    @torch.no_grad()
     def forward(self, x, y, is_stream=False):
-        rope_fn = getattr(dit, "FUSED_ROPE_FN", None)
-        if rope_fn is not None:
-            q = rope_fn(self.q(x), _unwrap(self.norm_q).weight, None,
-                        eps=_module_eps(self.norm_q), rope=False)
+        rope = getattr(dit, "FUSED_ROPE_FN", None)
+        if rope is None:
+            return stock(self, x, y, is_stream=is_stream)
+        q = rope(self.q(x), _inner(self.norm_q).weight, None, eps=_eps(self.norm_q), rope=False)
+        k, v = self.cache_k, self.cache_v
+        if k is None or v is None:
+            raise AssertionError("cross-attention needs the prompt K/V cached by init_cross_kv()")
+        if _on("FS89_CROSS_ATTN") and cross_supported(q, k, v, self.num_heads):
+            att = cross_attention(q, k, v, self.num_heads)
         else:
-            q = self.norm_q(self.q(x))
-        assert self.cache_k is not None and self.cache_v is not None
-        k = self.cache_k
-        v = self.cache_v
-        if _FLAG("FS89_CROSS_ATTN", "1") and cross_supported(q, k, v, self.num_heads):
-            x = cross_attention(q, k, v, self.num_heads)
-        else:
-            x = self.attn(q, k, v)
-        return self.o(x)
+            att = self.attn(q, k, v)
+        return self.o(att)
 
-    return torch.no_grad()(forward)
+    forward.__doc__ = ("CrossAttention.forward with the fused RMSNorm of q and dense attention "
+                       "over the cached prompt K/V on the HIP kernel (reference "
+                       "integrate.py:132-143); the upstream forward when FS89_FUSED_ROPE is off.")
+    return forward
 
 
-def _affine_layer_norm(m):
-    """(weight, bias, eps) when m is an affine nn.LayerNorm over bf16, else None."""
-    m = _unwrap(m)
+# ----------------------------------------------------------------------------- DiT block
+
+def _norm3_affine(m):
+    """(weight, bias, eps) when m is an affine LayerNorm over bf16 on the GPU, else None."""
+    m = _inner(m)
     if not isinstance(m, torch.nn.LayerNorm) or not m.elementwise_affine:
         return None
-    w, b = m.weight, m.bias
-    if w is None or w.dtype != torch.bfloat16 or not w.is_cuda:
+    if m.weight is None or m.weight.dtype != torch.bfloat16 or not m.weight.is_cuda:
         return None
-    return w, b, m.eps
+    return m.weight, m.bias, m.eps
 
 
-def _row_codes_block(dit, blk, x, f, h, w) -> bool:
-    """The DiT block runs the per-token FP8 dataflow of the C5 block (AdaLN
-    writing codes, one q/k/v GEMM, the copy-free self-attention): fused AdaLN
-    and RoPE on, the HIP attention, per-token q/k/v FP8 linears, batch-1 bf16
-    input in whole windows."""
+def _codes_dataflow(dit, blk, x, f, h, w) -> bool:
+    """Whether the block runs the per-token FP8 dataflow: the AdaLN writes the
+    q/k/v GEMM's codes, q/k/v are one GEMM, the self-attention is copy-free and
+    the cross residual is fused with the FFN's AdaLN.  Needs the fused AdaLN
+    and RoPE, the HIP attention, per-token q/k/v FP8 linears and a batch-1
+    bf16 input in whole windows."""
     sa = getattr(blk, "self_attn", None)
-    if sa is None or getattr(dit, "FUSED_ADALN", None) is None or \
-            getattr(dit, "FUSED_ROPE_FN", None) is None:
+    if sa is None or getattr(dit, "FUSED_ADALN", None) is None \
+            or getattr(dit, "FUSED_ROPE_FN", None) is None:
         return False
     if not (_window_path_on() and _window_path_ok(x, f, h, w, getattr(sa, "head_dim", 0))):
         return False
-    fq = _qkv_fused(sa)
-    return fq is not None and fq[3]
+    fused = _qkv_fused(sa)
+    return fused is not None and fused[3]
 
 
-def _make_dit_block_forward(dit):
-    """Fused-aware copy of upstream DiTBlock.forward (integrate.py:148-184)."""
+def _gated_residual_norm3(blk, x, gate, attn_out, gate_add):
+    """x + gate * attn_out and norm3 of the sum: one pass over the rows when
+    norm3 is an affine bf16 LayerNorm on the GPU, else the two steps."""
+    ln3 = _norm3_affine(blk.norm3)
+    bf16_gpu = x.dtype == torch.bfloat16 and x.is_cuda
+    if ln3 is not None and bf16_gpu and attn_out.is_contiguous() and gate.is_contiguous():
+        return fused_gate_add_layer_norm(x, gate, attn_out, ln3[0], ln3[1], eps=ln3[2])
+    x = gate_add(x, gate, attn_out)
+    normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2]) if ln3 is not None and bf16_gpu \
+        else blk.norm3(x)
+    return x, normed
 
+
+def _make_dit_block_forward(dit, stock):
     def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
                 train_img=False, block_id=None, kv_len=None, is_full_block=False,
                 is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
-        shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = (
-            self.modulation.to(dtype=t_mod.dtype, device=t_mod.device) + t_mod).chunk(6, dim=1)
-        fa = getattr(dit, "FUSED_ADALN", None)
-        if fa is not None:
-            ln_mod, gate_add = fa
-        rows = _row_codes_block(dit, self, x, f, h, w)
-        if rows:
-            # Per-token FP8 throughout: the AdaLN writes the codes the fused
-            # q/k/v GEMM takes (no bf16 round trip, one quantisation).
-            x8s = fused_ln_modulate_quant(x, scale_msa, shift_msa, eps=_module_eps(self.norm1))
-            r = _window_self_attention(dit, self.self_attn, x, freqs, f, h, w, topk, kv_len,
-                                       is_stream, pre_cache_k, pre_cache_v, local_range, x8s=x8s)
-            self_attn_output, self_attn_cache_k, self_attn_cache_v = (
-                r if is_stream else (r, None, None))
-        else:
-            if fa is not None:
-                input_x = ln_mod(x, scale_msa, shift_msa, eps=_module_eps(self.norm1))
-            else:
-                input_x = dit.modulate(self.norm1(x), shift_msa, scale_msa)
-            self_attn_output, self_attn_cache_k, self_attn_cache_v = self.self_attn(
-                input_x, freqs, f, h, w, local_num, topk, train_img, block_id,
-                kv_len=kv_len, is_full_block=is_full_block, is_stream=is_stream,
-                pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v, local_range=local_range)
+        adaln = getattr(dit, "FUSED_ADALN", None)
+        if adaln is None:
+            return stock(self, x, context, t_mod, freqs, f, h, w, local_num=local_num,
+                         topk=topk, train_img=train_img, block_id=block_id, kv_len=kv_len,
+                         is_full_block=is_full_block, is_stream=is_stream,
+                         pre_cache_k=pre_cache_k, pre_cache_v=pre_cache_v,
+                         local_range=local_range)
+        ln_mod, gate_add = adaln
+        m = Modulation(*(self.modulation.to(dtype=t_mod.dtype, device=t_mod.device)
+                         + t_mod).chunk(6, dim=1))
+        codes = _codes_dataflow(dit, self, x, f, h, w)
 
-        ln3 = _affine_layer_norm(self.norm3) if fa is not None else None
-        if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda and \
-                self_attn_output.is_contiguous() and gate_msa.is_contiguous():
-            # the gated residual and norm3 in one pass over the rows
-            x, normed = fused_gate_add_layer_norm(x, gate_msa, self_attn_output, ln3[0], ln3[1],
-                                                  eps=ln3[2])
+        # 1) self-attention on the modulated LayerNorm of x
+        if codes:
+            x8s = fused_ln_modulate_quant(x, m.scale_msa, m.shift_msa, eps=_eps(self.norm1))
+            r = _window_self_attention(dit, self.self_attn, x, freqs, f, h, w, topk, kv_len,
+                                       is_stream, pre_cache_k, pre_cache_v, local_range,
+                                       x8s=x8s)
         else:
-            if fa is not None:
-                x = gate_add(x, gate_msa, self_attn_output)
-            else:
-                x = self.gate(x, gate_msa, self_attn_output)
-            if ln3 is not None and x.dtype == torch.bfloat16 and x.is_cuda:
-                normed = layer_norm(x, ln3[0], ln3[1], eps=ln3[2])
-            else:
-                normed = self.norm3(x)
+            r = self.self_attn(ln_mod(x, m.scale_msa, m.shift_msa, eps=_eps(self.norm1)),
+                               freqs, f, h, w, local_num, topk, train_img, block_id,
+                               kv_len=kv_len, is_full_block=is_full_block,
+                               is_stream=is_stream, pre_cache_k=pre_cache_k,
+                               pre_cache_v=pre_cache_v, local_range=local_range)
+        attn_out, cache_k, cache_v = r if is_stream else (r, None, None)
+
+        # 2) gated residual, then the cross-attention on norm3 of it
+        x, normed = _gated_residual_norm3(self, x, m.gate_msa, attn_out, gate_add)
         yc = self.cross_attn(normed, context, is_stream=is_stream)
-        if rows and isinstance(self.ffn, FP8FFN) and yc.shape == x.shape and yc.is_contiguous():
-            # x + cross-attention output and the FFN's AdaLN in one pass (a
-            # unit gate), its per-token codes straight into the FFN's GEMMs.
+
+        # 3) FFN on the modulated LayerNorm of x + yc, gated residual
+        if codes and isinstance(self.ffn, FP8FFN) and yc.shape == x.shape and yc.is_contiguous():
+            # x + yc (a unit gate) and the FFN's AdaLN in one pass; its
+            # per-token codes go straight into the FFN GEMMs
             B, L, D = x.shape
             x, h8, hs = fused_gate_add_ln_modulate_quant(
-                x, unit_gate(D, x.device), yc, scale_mlp, shift_mlp, eps=_module_eps(self.norm2))
+                x, unit_gate(D, x.device), yc, m.scale_mlp, m.shift_mlp, eps=_eps(self.norm2))
             g8, gs = gemm_gelu_quant_fp8(h8, hs, self.ffn.lin0, True)
-            yf = self.ffn.lin2._mm(g8, gs)
-            x = gate_add(x, gate_mlp, yf.view(B, L, -1))
-            if is_stream:
-                return x, self_attn_cache_k, self_attn_cache_v
-            return x
-        x = x + yc
-        if fa is not None:
-            input_x = ln_mod(x, scale_mlp, shift_mlp, eps=_module_eps(self.norm2))
+            y = self.ffn.lin2._mm(g8, gs).view(B, L, -1)
         else:
-            input_x = dit.modulate(self.norm2(x), shift_mlp, scale_mlp)
-        if fa is not None:
-            x = gate_add(x, gate_mlp, self.ffn(input_x))
-        else:
-            x = self.gate(x, gate_mlp, self.ffn(input_x))
-        if is_stream:
-            return x, self_attn_cache_k, self_attn_cache_v
-        return x
+            x = x + yc
+            y = self.ffn(ln_mod(x, m.scale_mlp, m.shift_mlp, eps=_eps(self.norm2)))
+        x = gate_add(x, m.gate_mlp, y)
+        return (x, cache_k, cache_v) if is_stream else x
 
+    forward.__doc__ = ("DiTBlock.forward on the fused AdaLN / gated residual kernels "
+                       "(reference integrate.py:151-182); the upstream forward when "
+                       "FS89_FUSED_ADALN is off.")
     return forward
 
 
-_EXPECTED_SIGS = {
-    "SelfAttention": ("x", "freqs", "f", "h", "w", "local_num", "topk", "train_img",
-                      "block_id", "kv_len", "is_full_block", "is_stream",
-                      "pre_cache_k", "pre_cache_v", "local_range"),
-    "DiTBlock": ("x", "context", "t_mod", "freqs", "f", "h", "w", "local_num", "topk",
-                 "train_img", "block_id", "kv_len", "is_full_block", "is_stream",
-                 "pre_cache_k", "pre_cache_v", "local_range"),
-}
-
+# ----------------------------------------------------------------------------- patching
 
 def _check_dit_structure(dit):
-    """Guard against upstream drift (integrate.py:197-214): the rebound classes
-    must exist and keep the argument names the forwards pass positionally."""
-    import inspect
-    for cls, expected in _EXPECTED_SIGS.items():
-        c = getattr(dit, cls, None)
-        if c is None:
-            raise RuntimeError(f"upstream wan_video_dit has no {cls}; this pack "
-                               f"targets FlashVSR v1.1 — got {dit}")
-        params = tuple(inspect.signature(c.forward).parameters)
-        missing = [p for p in expected if p not in params]
-        if missing:
-            raise RuntimeError(
-                f"upstream {cls}.forward lacks args {missing} — upstream signature "
-                f"changed since the tested revision (cf910c6).")
-    if not hasattr(dit, "WindowPartition3D") or not hasattr(dit, "generate_draft_block_mask"):
-        raise RuntimeError("upstream wan_video_dit lacks WindowPartition3D / "
-                           "generate_draft_block_mask — unsupported revision.")
+    """Refuse an upstream DiT module this pack was not written against
+    (FlashVSR cf910c6; the reference guards the same, integrate.py:197-214):
+    each rebound class must exist with the argument names its forward is
+    called with, and the layout helpers the self-attention uses must exist."""
+    where = getattr(dit, "__name__", repr(dit))
+    for cls_name, wanted in _EXPECTED_SIGS.items():
+        cls = getattr(dit, cls_name, None)
+        if cls is None:
+            raise RuntimeError(f"{where} has no {cls_name}; the MI355X operator pack targets "
+                               "FlashVSR v1.1 (wan_video_dit at cf910c6)")
+        have = set(inspect.signature(cls.forward).parameters)
+        absent = [a for a in wanted if a not in have]
+        if absent:
+            raise RuntimeError(f"{where}.{cls_name}.forward lacks args {absent}: not the "
+                               "upstream revision (cf910c6) the rebound forwards follow")
+    absent = [n for n in _UPSTREAM_HELPERS if not hasattr(dit, n)]
+    if absent:
+        raise RuntimeError(f"{where} lacks {' / '.join(absent)}: unsupported upstream revision")
 
 
-def _patch_dit(dit, fused_rope, fused_adaln):
+def _patch_dit(dit, fused_rope: bool, fused_adaln: bool):
     _check_dit_structure(dit)
     dit.FUSED_ROPE_FN = fused_rms_rope if fused_rope else None
     dit.FUSED_ADALN = (fused_ln_modulate, fused_gate_add) if fused_adaln else None
     if getattr(dit, "_FS89_PATCHED", False):
-        return  # forwards already rebound; flags above refreshed
-    dit.SelfAttention.forward = _make_self_attn_forward(dit)
-    dit.CrossAttention.forward = _make_cross_attn_forward(dit)
-    dit.DiTBlock.forward = _make_dit_block_forward(dit)
+        return                      # forwards already rebound; the flags above are refreshed
+    stock = {n: getattr(dit, n).forward for n in _EXPECTED_SIGS}
+    setattr(dit, _STOCK_ATTR, stock)
+    dit.SelfAttention.forward = _make_self_attn_forward(dit, stock["SelfAttention"])
+    dit.CrossAttention.forward = _make_cross_attn_forward(dit, stock["CrossAttention"])
+    dit.DiTBlock.forward = _make_dit_block_forward(dit, stock["DiTBlock"])
     dit._FS89_PATCHED = True
+
+
+def _import_upstream_dit():
+    try:
+        import diffsynth.models.wan_video_dit as dit
+    except ImportError as e:
+        raise ImportError("enable() could not import diffsynth.models.wan_video_dit: run from a "
+                          "FlashVSR checkout, or pass dit_module=") from e
+    return dit
+
+
+def _setup_decoder(pipe, compile_memblocks: bool) -> dict:
+    done = {}
+    dec = getattr(pipe, "TCDecoder", None)
+    if dec is None:
+        return done
+    if _on("FS89_TCDEC_CL"):
+        dec.to(memory_format=torch.channels_last)
+        done["tcdec_channels_last"] = True
+    if compile_memblocks:
+        warnings.warn("FS89_TCDEC_COMPILE / compile_memblocks is not applied by the MI355X "
+                      "operator pack (decoder-side torch.compile is outside the pack).")
+        done["tcdec_compiled_memblocks"] = 0
+    return done
+
+
+def _setup_fp8(model, parts, per_row: bool, weights_file) -> dict:
+    done = {}
+    if not parts:
+        return done
+    stored = None
+    if weights_file and os.path.exists(weights_file):
+        stored = load_fp8_weights(weights_file)
+        done["fp8_weights"] = "loaded"
+    done["fp8_linears"] = convert_linears_fp8(model, parts=parts, per_channel=per_row,
+                                              per_token=per_row, stored=stored)
+    if weights_file and stored is None and done["fp8_linears"]:
+        save_fp8_weights(model, weights_file)
+        done["fp8_weights"] = "saved"
+    if "ffn" in parts and _on("FS89_FP8_FFNFUSED"):
+        done["fp8_ffn_blocks"] = convert_ffn_fp8(model)
+    return done
 
 
 def enable(pipe, dit_module=None, parts=None, compile_memblocks=None, verbose=True,
            scale_granularity=None, fp8_weights=None):
     """Apply the operator pack to a FlashVSRTinyPipeline; returns a dict of
-    what was enabled (same keys as the reference).  ``fp8_weights`` (or
-    ``FS89_FP8_WEIGHTS``) names a file of quantised weights: loaded instead of
-    quantising when it exists, written after the conversion when it does not
-    (then ``applied["fp8_weights"]`` says which)."""
+    what was enabled, with the reference's keys (integrate.py:229-292).
+
+    Extensions: ``scale_granularity`` ('tensor', the reference's default, or
+    'row'; env ``FS89_FP8_SCALE``) and ``fp8_weights`` (env
+    ``FS89_FP8_WEIGHTS``): a file of quantised weights, loaded instead of
+    quantising when it exists and written after the conversion when it does
+    not (``applied["fp8_weights"]`` says which)."""
     if parts is None:
         parts = [p for p in os.environ.get("FS89_FP8", "ffn,self,cross").split(",") if p]
     if compile_memblocks is None:
-        compile_memblocks = _FLAG("FS89_TCDEC_COMPILE", "0")
-    if scale_granularity is None:
-        scale_granularity = os.environ.get("FS89_FP8_SCALE", "tensor").lower()
-    if scale_granularity not in ("tensor", "row"):
-        raise ValueError(f"scale_granularity must be 'tensor' or 'row', got {scale_granularity!r}")
-    row = scale_granularity == "row"
-
-    applied = {}
-
-    if dit_module is None:
-        try:
-            import diffsynth.models.wan_video_dit as dit_module
-        except ImportError as e:
-            raise ImportError(
-                "enable() could not import diffsynth.models.wan_video_dit. Run from a "
-                "FlashVSR checkout (or pass dit_module=).") from e
-
-    if hasattr(pipe, "TCDecoder") and _FLAG("FS89_TCDEC_CL", "1"):
-        pipe.TCDecoder.to(memory_format=torch.channels_last)
-        applied["tcdec_channels_last"] = True
-
-    if compile_memblocks and hasattr(pipe, "TCDecoder"):
-        warnings.warn("FS89_TCDEC_COMPILE / compile_memblocks is not applied by the MI355X "
-                      "operator pack (decoder-side torch.compile is outside the pack).")
-        applied["tcdec_compiled_memblocks"] = 0
-
+        compile_memblocks = _on("FS89_TCDEC_COMPILE", "0")
+    granularity = (scale_granularity or os.environ.get("FS89_FP8_SCALE", "tensor")).lower()
+    if granularity not in ("tensor", "row"):
+        raise ValueError(f"scale_granularity must be 'tensor' or 'row', got {granularity!r}")
     if fp8_weights is None:
         fp8_weights = os.environ.get("FS89_FP8_WEIGHTS") or None
-    if parts:
-        stored = None
-        if fp8_weights and os.path.exists(fp8_weights):
-            stored = load_fp8_weights(fp8_weights)
-            applied["fp8_weights"] = "loaded"
-        n = convert_linears_fp8(pipe.denoising_model(), parts=parts, per_channel=row,
-                                per_token=row, stored=stored)
-        applied["fp8_linears"] = n
-        if fp8_weights and stored is None and n:
-            save_fp8_weights(pipe.denoising_model(), fp8_weights)
-            applied["fp8_weights"] = "saved"
-        if "ffn" in parts and _FLAG("FS89_FP8_FFNFUSED", "1"):
-            applied["fp8_ffn_blocks"] = convert_ffn_fp8(pipe.denoising_model())
+    dit = dit_module if dit_module is not None else _import_upstream_dit()
 
-    _patch_dit(dit_module,
-               fused_rope=_FLAG("FS89_FUSED_ROPE", "1"),
-               fused_adaln=_FLAG("FS89_FUSED_ADALN", "1"))
-    applied["fused_rope"] = _FLAG("FS89_FUSED_ROPE", "1")
-    applied["fused_adaln"] = _FLAG("FS89_FUSED_ADALN", "1")
-
+    applied = _setup_decoder(pipe, compile_memblocks)
+    applied.update(_setup_fp8(pipe.denoising_model(), parts, granularity == "row", fp8_weights))
+    rope_on, adaln_on = _on("FS89_FUSED_ROPE"), _on("FS89_FUSED_ADALN")
+    _patch_dit(dit, fused_rope=rope_on, fused_adaln=adaln_on)
+    applied["fused_rope"] = rope_on
+    applied["fused_adaln"] = adaln_on
     ensure_bsa_available()
     applied["lcsa_backend"] = active_backend()
-
     if verbose:
-        bits = [f"{k}={v}" for k, v in applied.items()]
-        print(f"[flashvsr-mi355x-ops] enabled: {', '.join(bits)}")
+        print("[flashvsr-mi355x-ops] enabled: " + ", ".join(f"{k}={v}" for k, v in applied.items()))
     return applied

@@ -42,11 +42,40 @@ def build_csr(keep: torch.Tensor):
     return sel, cnt, max(NK, 1)
 
 
+def _check_extent(t, rows: int, tok_stride: int, head_stride: int, heads: int, head_dim: int,
+                  name: str):
+    """t's storage holds `rows` tokens of `heads` heads at the given strides."""
+    if rows <= 0:
+        return
+    need = (rows - 1) * tok_stride + (heads - 1) * head_stride + head_dim
+    have = t.untyped_storage().nbytes() // t.element_size() - t.storage_offset()
+    if min(tok_stride, head_stride) < 0 or need > have:
+        raise ValueError(f"{name}: {rows} tokens x {heads} heads at strides ({tok_stride}, "
+                         f"{head_stride}) need {need} elements, its storage holds {have}")
+
+
+def _check_index(sel, cnt, maxk, H, NQ):
+    for t, n in ((sel, "sel"), (cnt, "cnt")):
+        _lib.require_dtype(t, torch.int32, n)
+        if not t.is_contiguous():
+            raise ValueError(f"block index {n} must be contiguous")
+    if cnt.numel() != H * NQ or sel.numel() < H * NQ * maxk or maxk < 0:
+        raise ValueError(f"block index of {tuple(sel.shape)} / {tuple(cnt.shape)} entries does "
+                         f"not cover {H} heads x {NQ} query blocks x {maxk} key blocks")
+
+
 def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, head_dim: int,
                                    q_strides, kv_strides, out=None, o_strides=None,
                                    q_map=None, kv_map=None, index=None):
     """General entry: q/k/v/out bf16 with (token stride, head stride) in
-    elements; keep [H, NQ, NK] (or a prebuilt ``index=(sel, cnt, maxk)``)."""
+    elements; keep [H, NQ, NK] (or a prebuilt ``index=(sel, cnt, maxk)``).
+
+    Checked before the launch: the index covers H x NQ rows of maxk entries
+    (contiguous int32); without maps, q/out hold NQ*128 tokens and k/v NK*128
+    at their strides; maps are int32 with at least NQ*128 / NK*128 entries.
+    Not checked (a host sync would be needed): that map entries lie inside
+    their tensors and that sel/cnt values lie inside [0, NK) / [0, maxk], as
+    build_csr and the device draft mask produce them."""
     _lib.require_gpu(q, k, v, out, q_map, kv_map)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _lib.require_dtype(t, torch.bfloat16, n)
@@ -59,14 +88,27 @@ def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, 
         NK = maxk
     if H != heads:
         raise ValueError(f"block mask has {H} heads, tensors have {heads}")
+    _lib.require_gpu(sel, cnt)
+    _check_index(sel, cnt, maxk, H, NQ)
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(head_dim)
     if out is None:
         raise ValueError("out is required")
+    _lib.require_dtype(out, torch.bfloat16, "out")
     o_strides = o_strides or q_strides
-    for m in (q_map, kv_map):
-        if m is not None:
+    if (q_map is None) != (kv_map is None):
+        raise ValueError("token maps come in pairs (q_map with kv_map)")
+    if q_map is None:
+        _check_extent(q, NQ * BLOCK, *q_strides, heads, head_dim, "q")
+        _check_extent(out, NQ * BLOCK, *o_strides, heads, head_dim, "out")
+        _check_extent(k, NK * BLOCK, *kv_strides, heads, head_dim, "k")
+        _check_extent(v, NK * BLOCK, *kv_strides, heads, head_dim, "v")
+    else:
+        for m, n, want in ((q_map, "q_map", NQ * BLOCK), (kv_map, "kv_map", NK * BLOCK)):
             _lib.require_dtype(m, torch.int32, "token map")
+            if not m.is_contiguous() or m.numel() < want:
+                raise ValueError(f"{n} must be contiguous with at least {want} entries, "
+                                 f"got {m.numel()}")
     rc = _lib.lib().fvsr_bsa_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
         q_strides[0], q_strides[1], kv_strides[0], kv_strides[1], o_strides[0], o_strides[1],

@@ -52,7 +52,8 @@ enum {
 /* Library version string ("fvsr <semver> gfx950"). */
 const char* fvsr_version(void);
 
-/* Number of 32-bit floats of workspace quant entry points need. */
+/* Number of 32-bit floats of workspace the quant entry points need: the
+ * per-tensor partial maxima; 0 for FVSR_SCALE_ROW (no workspace, may be NULL). */
 int64_t fvsr_quant_workspace_floats(int64_t rows, int64_t cols, int mode);
 
 /*

@@ -135,19 +135,24 @@ def test_bsa_stub_rejects_unsupported(kw):
 # ----------------------------------------------------------------------------- integrate
 
 def make_fake_dit():
-    """A stand-in for diffsynth.models.wan_video_dit with the rebound classes,
-    stock helpers in torch, and the upstream forward signatures."""
+    """A stand-in for diffsynth.models.wan_video_dit: the rebound classes with
+    the upstream forward signatures, stock forwards that compute the upstream
+    math in torch (CrossAttention, DiTBlock) and record that they ran, and the
+    stock helpers."""
     dit = types.ModuleType("fake_wan_video_dit")
+    dit.stock_calls = []
 
     class SelfAttention(torch.nn.Module):
         def forward(self, x, freqs, f=None, h=None, w=None, local_num=None, topk=None,
                     train_img=False, block_id=None, kv_len=None, is_full_block=False,
                     is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
-            raise AssertionError("stock forward must be rebound")
+            dit.stock_calls.append("SelfAttention")
+            raise NotImplementedError("stock self-attention is not modelled here")
 
     class CrossAttention(torch.nn.Module):
         def forward(self, x, y, is_stream=False):
-            raise AssertionError
+            dit.stock_calls.append("CrossAttention")
+            return self.o(self.attn(self.norm_q(self.q(x)), self.cache_k, self.cache_v))
 
     class DiTBlock(torch.nn.Module):
         def __init__(self, dim=16):
@@ -160,7 +165,16 @@ def make_fake_dit():
         def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
                     train_img=False, block_id=None, kv_len=None, is_full_block=False,
                     is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
-            raise AssertionError
+            dit.stock_calls.append("DiTBlock")
+            sh, sc, g, sh2, sc2, g2 = (self.modulation + t_mod).chunk(6, dim=1)
+            a, ck, cv = self.self_attn(dit.modulate(self.norm1(x), sh, sc), freqs, f, h, w,
+                                       local_num, topk, train_img, block_id, kv_len=kv_len,
+                                       is_stream=is_stream, pre_cache_k=pre_cache_k,
+                                       pre_cache_v=pre_cache_v, local_range=local_range)
+            x = self.gate(x, g, a)
+            x = x + self.cross_attn(self.norm3(x), context, is_stream=is_stream)
+            x = self.gate(x, g2, self.ffn(dit.modulate(self.norm2(x), sh2, sc2)))
+            return (x, ck, cv) if is_stream else x
 
         def gate(self, x, gate, residual):
             return x + gate * residual
@@ -210,11 +224,12 @@ def test_enable_wiring_flags_and_idempotence(monkeypatch, capsys):
     import flashvsr_sm89_ops as f
     from flashvsr_sm89_ops import integrate
     dit = make_fake_dit()
-    stock = dit.SelfAttention.forward
+    stock = {n: getattr(dit, n).forward for n in ("SelfAttention", "CrossAttention", "DiTBlock")}
     monkeypatch.setenv("FS89_FP8", "")
     applied = f.enable(FakePipe(), dit_module=dit)
     assert applied == {"fused_rope": True, "fused_adaln": True, "lcsa_backend": "hip"}
-    assert dit.SelfAttention.forward is not stock and dit._FS89_PATCHED
+    assert dit.SelfAttention.forward is not stock["SelfAttention"] and dit._FS89_PATCHED
+    assert dit._FS89_STOCK == stock          # the upstream forwards, captured before rebinding
     assert dit.FUSED_ROPE_FN is f.fused_rms_rope
     assert dit.FUSED_ADALN == (f.fused_ln_modulate, f.fused_gate_add)
     assert "[flashvsr-mi355x-ops] enabled" in capsys.readouterr().out
@@ -224,6 +239,7 @@ def test_enable_wiring_flags_and_idempotence(monkeypatch, capsys):
     applied = f.enable(FakePipe(), dit_module=dit, verbose=False)
     assert applied["fused_rope"] is False and dit.FUSED_ROPE_FN is None and dit.FUSED_ADALN is None
     assert dit.DiTBlock.forward is rebound  # not rebound twice
+    assert dit._FS89_STOCK == stock          # still the upstream ones, not the rebound ones
     with pytest.raises(ValueError):
         f.enable(FakePipe(), dit_module=dit, scale_granularity="block")
     monkeypatch.setitem(sys.modules, "diffsynth", None)
@@ -232,8 +248,9 @@ def test_enable_wiring_flags_and_idempotence(monkeypatch, capsys):
 
 
 def test_stock_branch_dit_block_on_cpu(monkeypatch):
-    """With the fused flags off, the rebound DiTBlock.forward is the stock
-    math: AdaLN(shift, scale) order, gate, cross-attention residual."""
+    """With the fused flags off, the rebound DiTBlock.forward is the upstream
+    forward captured by enable(): AdaLN(shift, scale) order, gate,
+    cross-attention residual."""
     import flashvsr_sm89_ops as f
     dit = make_fake_dit()
     monkeypatch.setenv("FS89_FP8", "")
@@ -251,7 +268,8 @@ def test_stock_branch_dit_block_on_cpu(monkeypatch):
     blk.ffn = lambda x: x - 1
     x = torch.randn(1, 5, 16)
     t_mod = torch.randn(1, 6, 16) * 0.1
-    out = blk(x, None, t_mod, None, 1, 1, 5)
+    out, ck, cv = blk(x, None, t_mod, None, 1, 1, 5, is_stream=True)
+    assert dit.stock_calls == ["DiTBlock"] and ck is None and cv is None
     sh, sc, g, sh2, sc2, g2 = (blk.modulation + t_mod).chunk(6, dim=1)
     ln = torch.nn.functional.layer_norm
     a_in = ln(x, (16,), eps=1e-6) * (1 + sc) + sh
@@ -260,6 +278,50 @@ def test_stock_branch_dit_block_on_cpu(monkeypatch):
     x1 = x1 + (ln(x1, (16,), weight=blk.norm3.weight, bias=blk.norm3.bias, eps=1e-6) * 0 + 1)
     ref = x1 + g2 * ((ln(x1, (16,), eps=1e-6) * (1 + sc2) + sh2) - 1)
     torch.testing.assert_close(out, ref)
+
+
+def test_stock_self_attention_when_rope_off(monkeypatch):
+    """FS89_FUSED_ROPE=0: the rebound SelfAttention.forward hands every
+    argument to the upstream forward by name."""
+    import flashvsr_sm89_ops as f
+    dit = make_fake_dit()
+    got = {}
+
+    def upstream(self, x, freqs, f=None, h=None, w=None, local_num=None, topk=None,
+                 train_img=False, block_id=None, kv_len=None, is_full_block=False,
+                 is_stream=False, pre_cache_k=None, pre_cache_v=None, local_range=9):
+        got.update(locals())
+        return "stock"
+    dit.SelfAttention.forward = upstream
+    monkeypatch.setenv("FS89_FP8", "")
+    monkeypatch.setenv("FS89_FUSED_ROPE", "0")
+    f.enable(FakePipe(), dit_module=dit, verbose=False)
+    sa = dit.SelfAttention()
+    x = torch.zeros(1, 4, 8)
+    assert sa(x, "fr", 2, 1, 2, 3, 4, True, 5, kv_len=6, is_full_block=True, is_stream=True,
+              pre_cache_k="k", pre_cache_v="v", local_range=7) == "stock"
+    assert got["x"] is x and (got["freqs"], got["f"], got["h"], got["w"]) == ("fr", 2, 1, 2)
+    assert (got["local_num"], got["topk"], got["train_img"], got["block_id"]) == (3, 4, True, 5)
+    assert (got["kv_len"], got["is_full_block"], got["is_stream"]) == (6, True, True)
+    assert (got["pre_cache_k"], got["pre_cache_v"], got["local_range"]) == ("k", "v", 7)
+
+
+def test_fused_self_attention_checks_stream_geometry(monkeypatch):
+    """The fused self-attention keeps the upstream preconditions: a stream
+    starts with 6 latent frames, continues with 2, and L == f*h*w."""
+    import flashvsr_sm89_ops as f
+    dit = make_fake_dit()
+    monkeypatch.setenv("FS89_FP8", "")
+    f.enable(FakePipe(), dit_module=dit, verbose=False)
+    sa = dit.SelfAttention()
+    sa.head_dim = 128
+    x = torch.zeros(1, 2 * 8 * 8, 256)
+    with pytest.raises(AssertionError, match="f == 6"):
+        sa(x, None, 2, 8, 8, is_stream=True)
+    with pytest.raises(AssertionError, match="f == 2"):
+        sa(torch.zeros(1, 6 * 64, 256), None, 6, 8, 8, is_stream=True, pre_cache_k=x, pre_cache_v=x)
+    with pytest.raises(AssertionError, match="sequence length"):
+        sa(x, None, 2, 8, 4)
 
 
 def test_window_token_map_matches_partition():
@@ -272,11 +334,9 @@ def test_window_token_map_matches_partition():
 
 
 def test_stock_branch_cross_attention_on_cpu(monkeypatch):
-    """The rebound CrossAttention.forward keeps the DiT's own attention where
-    the HIP kernel does not apply (here: CPU tensors), with the stock RMSNorm
-    when the fused flag is off (integrate.py:132-143)."""
+    """FS89_FUSED_ROPE=0: the rebound CrossAttention.forward is the upstream
+    forward (stock RMSNorm, the DiT's own attention over the cached K/V)."""
     import flashvsr_sm89_ops as f
-    from flashvsr_sm89_ops.cross_attn import supported
     dit = make_fake_dit()
     monkeypatch.setenv("FS89_FP8", "")
     monkeypatch.setenv("FS89_FUSED_ROPE", "0")
@@ -295,14 +355,49 @@ def test_stock_branch_cross_attention_on_cpu(monkeypatch):
     ca.attn = attn
     x = torch.randn(1, 5, 16)
     out = ca(x, None)
+    assert dit.stock_calls == ["CrossAttention"]
     q, k, v = seen["args"]
     torch.testing.assert_close(q, ca.q(x) * 3)
     assert k is ca.cache_k and v is ca.cache_v
     torch.testing.assert_close(out, ca.o(ca.q(x) * 3 + 1))
-    assert not supported(q, k, v, 2)
 
 
-def _dit_like(dim=16, ffn=32):
+def test_fused_cross_attention_keeps_dit_attention_where_kernel_does_not_apply(monkeypatch):
+    """FS89_FUSED_ROPE on: q's RMSNorm goes through FUSED_ROPE_FN (rope=False);
+    shapes the HIP attention does not cover (here CPU tensors) use the DiT's
+    own attention; a missing prompt cache is refused."""
+    import flashvsr_sm89_ops as f
+    from flashvsr_sm89_ops.cross_attn import supported
+    dit = make_fake_dit()
+    monkeypatch.setenv("FS89_FP8", "")
+    f.enable(FakePipe(), dit_module=dit, verbose=False)
+    calls = []
+
+    def fake_rms(x, weight, freqs, eps=1e-6, rope=True, head_dim=128):
+        calls.append((freqs, eps, rope))
+        return x * 3
+    monkeypatch.setattr(dit, "FUSED_ROPE_FN", fake_rms)
+    ca = dit.CrossAttention()
+    ca.q, ca.o = torch.nn.Linear(16, 16), torch.nn.Linear(16, 16)
+    ca.norm_q = torch.nn.Module()
+    ca.norm_q.weight, ca.norm_q.eps = torch.ones(16), 1e-5
+    ca.num_heads = 2
+    ca.cache_k, ca.cache_v = torch.randn(1, 7, 16), torch.randn(1, 7, 16)
+    ca.attn = lambda q, k, v: q + 1
+    x = torch.randn(1, 5, 16)
+    out = ca(x, None)
+    assert calls == [(None, 1e-5, False)] and dit.stock_calls == []
+    torch.testing.assert_close(out, ca.o(ca.q(x) * 3 + 1))
+    assert not supported(ca.q(x), ca.cache_k, ca.cache_v, 2)
+    ca.cache_k = None
+    with pytest.raises(AssertionError, match="init_cross_kv"):
+        ca(x, None)
+
+
+def _dit_like(dim=16, ffn=32, seed=0):
+    """Two DiT blocks' worth of Linears; the same seed gives the same weights
+    (the same checkpoint)."""
+    torch.manual_seed(seed)
     m = torch.nn.Module()
     m.blocks = torch.nn.ModuleList()
     for _ in range(2):
@@ -377,15 +472,42 @@ def test_fp8_weights_rejects_mismatch(tmp_path):
         load_fp8_weights(other)
 
 
+def test_fp8_weights_from_other_checkpoint_refused(tmp_path):
+    """A weight file saved from one checkpoint is refused for a model of the
+    same architecture whose weights (or biases) differ: the per-module source
+    fingerprints in the file's metadata do not match."""
+    from flashvsr_sm89_ops.fp8_linear import (convert_linears_fp8, load_fp8_weights,
+                                              save_fp8_weights, source_fingerprint)
+    src = _dit_like(seed=0)
+    convert_linears_fp8(src, parts=("self", "ffn"), stored=_stored_for(src, per_channel=False))
+    path = str(tmp_path / "w.safetensors")
+    save_fp8_weights(src, path)
+    back = load_fp8_weights(path)
+    assert convert_linears_fp8(_dit_like(seed=0), parts=("self", "ffn"), stored=back) == 12
+    with pytest.raises(ValueError, match="fingerprint"):
+        convert_linears_fp8(_dit_like(seed=1), parts=("self", "ffn"), stored=back)
+    bias_only = _dit_like(seed=0)
+    with torch.no_grad():
+        bias_only.blocks[1].ffn[0].bias[3] += 1e-3
+    with pytest.raises(ValueError, match="blocks.1.ffn.0"):
+        convert_linears_fp8(bias_only, parts=("self", "ffn"), stored=back)
+    # the fingerprint sees a swap of two weights (a plain sum would not)
+    w = torch.randn(4, 8)
+    w2 = w.clone()
+    w2[0, 0], w2[3, 7] = w[3, 7], w[0, 0]
+    assert source_fingerprint(w, None) != source_fingerprint(w2, None)
+    assert source_fingerprint(w, None) == source_fingerprint(w.clone(), None)
+
+
 def test_enable_loads_stored_fp8_weights(tmp_path, monkeypatch):
     import flashvsr_sm89_ops as f
     from flashvsr_sm89_ops.fp8_linear import convert_linears_fp8, save_fp8_weights
-    src = _dit_like()
+    src = _dit_like(seed=4)
     convert_linears_fp8(src, parts=("self", "ffn"), stored=_stored_for(src, per_channel=False))
     path = str(tmp_path / "w.safetensors")
     save_fp8_weights(src, path)
     pipe = FakePipe()
-    pipe.model = _dit_like()
+    pipe.model = _dit_like(seed=4)
     monkeypatch.setenv("FS89_FP8", "self")
     monkeypatch.setenv("FS89_FP8_WEIGHTS", path)
     applied = f.enable(pipe, dit_module=make_fake_dit(), verbose=False)
@@ -483,3 +605,101 @@ def test_qkv_fusion_weight_assembly():
     assert _qkv_fused(types.SimpleNamespace(q=mod.q, k=mod.k, v=lin(torch.tensor(1.0),
                                                                    bias=False))) is None
     assert _qkv_fused(types.SimpleNamespace(q=mod.q, k=mod.k, v=torch.nn.Linear(8, 4))) is None
+
+
+def test_rope_table_cache_follows_tensor_identity():
+    """The complex128 -> (cos, sin) table cache never serves a table to a
+    different freqs tensor, even one allocated at a freed tensor's address,
+    and rebuilds after an in-place change."""
+    from flashvsr_sm89_ops.fused_rms_rope import _freqs_table
+    g = torch.Generator().manual_seed(3)
+    for _ in range(20):
+        ang = torch.rand(48, 64, generator=g, dtype=torch.float64) * 6.28
+        fr = torch.polar(torch.ones_like(ang), ang)           # complex128, like Wan's freqs
+        t = _freqs_table(fr)
+        want = torch.view_as_real(fr.to(torch.complex64))
+        assert torch.equal(t, want)
+        assert _freqs_table(fr) is t                          # same live tensor: cached
+        del fr, t                                             # the next one may reuse the address
+    fr = torch.polar(torch.ones(8, 64, dtype=torch.float64), torch.zeros(8, 64, dtype=torch.float64))
+    t0 = _freqs_table(fr)
+    fr.mul_(1j)                                               # in place: rotate by 90 degrees
+    t1 = _freqs_table(fr)
+    assert t1 is not t0 and torch.equal(t1, torch.view_as_real(fr.to(torch.complex64)))
+
+
+def test_qkv_fusion_not_fooled_by_reused_addresses():
+    """A q/k/v FP8Linear replaced by a new one (whose tensors may sit at the
+    freed tensors' addresses, version 0 again) rebuilds the fused weight."""
+    import gc
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    from flashvsr_sm89_ops.integrate import _qkv_fused
+    g = torch.Generator().manual_seed(1)
+
+    def lin(fill):
+        w8 = torch.full((4, 8), fill, dtype=torch.uint8)
+        return FP8Linear.from_quantized(w8, torch.tensor(0.5), torch.zeros(4, dtype=torch.bfloat16))
+
+    mod = types.SimpleNamespace(q=lin(1), k=lin(2), v=lin(3))
+    for fill in range(4, 24):
+        _qkv_fused(mod)
+        mod.k = None
+        gc.collect()
+        mod.k = lin(fill)
+        w3 = _qkv_fused(mod)[0]
+        assert torch.equal(w3[4:8].view(torch.uint8), torch.full((4, 8), fill, dtype=torch.uint8))
+
+
+def test_bsa_wrapper_size_checks():
+    """Host-side checks of block_sparse_attention_strided that run before the
+    launch: tensor extents at the given strides, the block index's size and
+    dtype (a mismatch would make the kernel read out of bounds)."""
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import _check_extent, _check_index
+    H, D, NQ = 2, 128, 3
+    q = torch.empty(NQ * 128, H * D, dtype=torch.bfloat16)
+    _check_extent(q, NQ * 128, H * D, D, H, D, "q")
+    _check_extent(q[1:], NQ * 128 - 1, H * D, D, H, D, "q")            # a view: its own extent
+    with pytest.raises(ValueError, match="q: 384 tokens"):
+        _check_extent(q[1:], NQ * 128, H * D, D, H, D, "q")
+    with pytest.raises(ValueError, match="storage holds"):
+        _check_extent(q, NQ * 128, H * D, D, H + 1, D, "q")           # one head too many
+    # column slice of a fused [L, 3D] tensor: rows 3D apart, the last slice ends at the end
+    qkv = torch.empty(NQ * 128, 3 * H * D, dtype=torch.bfloat16)
+    _check_extent(qkv[:, 2 * H * D:], NQ * 128, 3 * H * D, D, H, D, "v")
+    with pytest.raises(ValueError):
+        _check_extent(qkv[:, 2 * H * D + 8:], NQ * 128, 3 * H * D, D, H, D, "v")
+    sel = torch.zeros(H, NQ, 4, dtype=torch.int32)
+    cnt = torch.zeros(H, NQ, dtype=torch.int32)
+    _check_index(sel, cnt, 4, H, NQ)
+    with pytest.raises(ValueError, match="does not cover"):
+        _check_index(sel, cnt, 5, H, NQ)                                # maxk beyond sel rows
+    with pytest.raises(ValueError, match="does not cover"):
+        _check_index(sel, cnt[:, :2].contiguous(), 4, H, NQ)
+    with pytest.raises(TypeError):
+        _check_index(sel.long(), cnt, 4, H, NQ)
+    with pytest.raises(ValueError, match="contiguous"):
+        _check_index(sel.transpose(0, 1), cnt, 4, H, NQ)
+
+
+def test_convert_ffn_fp8_swap_and_assertion():
+    """convert_ffn_fp8 (reference fp8_ffn.py:99-115): every blocks.<i>.ffn
+    Sequential over FP8Linears becomes an FP8FFN holding those two modules;
+    FFNs whose Linears are not FP8 yet raise AssertionError; a second call
+    replaces nothing; modules outside blocks.<i>.ffn are untouched."""
+    from flashvsr_sm89_ops.fp8_ffn import FP8FFN, convert_ffn_fp8
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear, convert_linears_fp8
+    plain = _dit_like()
+    with pytest.raises(AssertionError, match="blocks.0.ffn"):
+        convert_ffn_fp8(plain)
+    model = _dit_like()
+    model.head = torch.nn.Sequential(torch.nn.Linear(16, 16), torch.nn.GELU(),
+                                     torch.nn.Linear(16, 16))
+    convert_linears_fp8(model, parts=("ffn",), stored=_stored_for(model, per_channel=False))
+    ups = [b.ffn[0] for b in model.blocks]
+    downs = [b.ffn[2] for b in model.blocks]
+    assert convert_ffn_fp8(model) == 2
+    for b, up, down in zip(model.blocks, ups, downs):
+        assert isinstance(b.ffn, FP8FFN) and b.ffn.lin0 is up and b.ffn.lin2 is down
+        assert isinstance(up, FP8Linear) and isinstance(down, FP8Linear)
+    assert isinstance(model.head, torch.nn.Sequential)
+    assert convert_ffn_fp8(model) == 0
