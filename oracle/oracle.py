@@ -148,16 +148,18 @@ def fp8_gemm(a8: np.ndarray, sa: np.ndarray, b8: np.ndarray, sb: np.ndarray,
 
     Restates torch._scaled_mm(x8, W8.t(), scale_a, scale_b, bias, bf16) at
     fp8_linear.py:28-30; fp8*fp8 products are exact, so with float64
-    accumulation the only freedom left is the final rounding.
+    accumulation the only freedom left is the final rounding.  ``acc_dtype``
+    float32 (for the full-size checks) keeps the products exact and rounds
+    the sums: the bf16 result then differs from the float64 one only where the
+    exact value lies within ~1e-6 (relative) of a bf16 rounding boundary.
     ``sa`` is [1] or [M]; ``sb`` is [1] or [N]."""
     A = e4m3_decode(a8).astype(acc_dtype)
     B = e4m3_decode(b8).astype(acc_dtype)
-    acc = A @ B.T
-    sa = np.asarray(sa, np.float32).reshape(-1, 1).astype(acc_dtype)
-    sb = np.asarray(sb, np.float32).reshape(1, -1).astype(acc_dtype)
-    y = acc * sa * sb
+    y = A @ B.T
+    y *= np.asarray(sa, np.float32).reshape(-1, 1).astype(acc_dtype)
+    y *= np.asarray(sb, np.float32).reshape(1, -1).astype(acc_dtype)
     if bias is not None:
-        y = y + np.asarray(bias, np.float32).reshape(1, -1)
+        y += np.asarray(bias, np.float32).reshape(1, -1)
     return bf16(y.astype(np.float32))
 
 
@@ -488,49 +490,118 @@ def cross_attention_block(x, norm3_w, norm3_b, params_q, norm_q_w, cache_k, cach
 # DiT block composition (the C5 unit; integrate.py:151-182 with 47-124)
 # ----------------------------------------------------------------------------
 
-def linear_fp8(x: np.ndarray, wq, ws, bias, per_token: bool = True) -> np.ndarray:
+def quantize_input(x_bits: np.ndarray, per_token: bool = False, contiguous: bool = True):
+    """The activation quantisation of FP8Linear.forward / FP8FFN.forward
+    (fp8_linear.py:35-40, fp8_ffn.py:88-92): quantize_fp8 for a contiguous
+    input; for a non-contiguous one the reference's eager expression
+    ``s = (x2.abs().amax() / 448).clamp(min=1e-12).float(); (x2 / s).to(e4m3)``
+    on bf16 tensors, which rounds the scale and x/s to bf16 - the per-tensor
+    weight formula Q-W.  Per-token scales (the BASELINE extension) have one
+    form only."""
+    if per_token or contiguous:
+        return quantize_fp8(x_bits, per_row=per_token)
+    return quantize_weight(x_bits, per_channel=False)
+
+
+def linear_fp8(x: np.ndarray, wq, ws, bias, per_token: bool = True,
+               contiguous: bool = True, acc=np.float64) -> np.ndarray:
     """FP8Linear.forward (fp8_linear.py:32-42) on [T, K] bf16 values."""
-    q, s = quantize_fp8(bf16_bits(x), per_row=per_token)
-    return fp8_gemm(q, s, wq, ws, bias)
+    q, s = quantize_input(bf16_bits(x), per_token, contiguous)
+    return fp8_gemm(q, s, wq, ws, bias, acc_dtype=acc)
 
 
-def ffn_fp8(x: np.ndarray, w1q, w1s, b1, w2q, w2s, b2, per_token: bool = True) -> np.ndarray:
+def ffn_fp8(x: np.ndarray, w1q, w1s, b1, w2q, w2s, b2, per_token: bool = True,
+            contiguous: bool = True, acc=np.float64) -> np.ndarray:
     """FP8FFN.forward (fp8_ffn.py:84-96): quant -> mm0 -> GELU requant -> mm2."""
-    q, s = quantize_fp8(bf16_bits(x), per_row=per_token)
-    h = fp8_gemm(q, s, w1q, w1s, b1)
+    q, s = quantize_input(bf16_bits(x), per_token, contiguous)
+    h = fp8_gemm(q, s, w1q, w1s, b1, acc_dtype=acc)
     hq, hs = quantize_fp8(bf16_bits(h), per_row=per_token, gelu=True)
-    return fp8_gemm(hq, hs, w2q, w2s, b2)
+    return fp8_gemm(hq, hs, w2q, w2s, b2, acc_dtype=acc)
+
+
+def self_attention(xin, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6,
+                   per_token: bool = True, cache=None, kv_len=None, windows=None,
+                   acc=np.float64):
+    """The DiT self-attention (integrate.py:47-124) on [L, dim] bf16 values:
+    FP8 q/k/v -> RMSNorm+RoPE(q, k) -> window partition (2,8,8) -> cached
+    windows in front of k and v -> block-sparse attention (kept blocks
+    ``keep`` [heads, NQ, NK], NK counting the cached windows) -> reverse ->
+    FP8 o.  ``cache`` = (k_w, v_w) window-ordered [windows, 128, dim]; the
+    returned cache drops the oldest step's windows once it holds more than
+    ``kv_len`` steps (integrate.py:81-83,108-115).
+    ``windows`` (per-token scales only, where rows are independent outside
+    the attention): evaluate q, the attention and o only for the tokens of
+    these query windows; o then holds those tokens' rows, in window order.
+    Returns (o, cache_k, cache_v)."""
+    f, h, w = fhw
+    L, dim = xin.shape
+    hd = dim // heads
+    k, v = (linear_fp8(xin, *params[n], per_token=per_token, acc=acc) for n in ("k", "v"))
+    k = rms_rope(k[None], params["norm_k"], cos, sin, eps)[0]
+    kw, vw = (window_partition(t.reshape(1, f, h, w, dim)) for t in (k, v))
+    if windows is None:
+        q = linear_fp8(xin, *params["q"], per_token=per_token, acc=acc)
+        qw = window_partition(rms_rope(q[None], params["norm_q"], cos, sin, eps)[0]
+                              .reshape(1, f, h, w, dim))
+        qkeep = keep
+    else:
+        assert per_token, "a window subset needs row-local (per-token) quantisation"
+        tok = window_tokens(fhw, windows)
+        q = linear_fp8(xin[tok], *params["q"], per_token=True, acc=acc)
+        qw = rms_rope(q[None], params["norm_q"], np.asarray(cos)[tok], np.asarray(sin)[tok],
+                      eps)[0].reshape(-1, 128, dim)
+        qkeep = np.asarray(keep)[:, windows]
+    per_step = kw.shape[0] // (f // 2)
+    if cache is not None:
+        kw = np.concatenate([cache[0], kw])
+        vw = np.concatenate([cache[1], vw])
+    att = bf16(sparse_attention(qw.reshape(-1, heads, hd), kw.reshape(-1, heads, hd),
+                                vw.reshape(-1, heads, hd), qkeep))
+    if windows is None:
+        att = window_reverse(att.reshape(-1, 128, dim), (f, h, w))[0]
+    else:
+        att = att.reshape(-1, dim)
+    o = linear_fp8(att, *params["o"], per_token=per_token, acc=acc)
+    if kv_len is not None and kw.shape[0] // per_step > kv_len:
+        kw, vw = kw[per_step:], vw[per_step:]
+    return o, kw, vw
+
+
+def window_tokens(fhw, windows) -> np.ndarray:
+    """Raster token indices of the given windows' tokens, in window order."""
+    f, h, w = fhw
+    order = window_partition(np.arange(f * h * w, dtype=np.float32).reshape(1, f, h, w, 1))
+    return order[np.asarray(windows)].reshape(-1).astype(np.int64)
 
 
 def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6,
-              cross=None):
-    """One DiT block of the C5 stack on [L, dim] bf16 values (batch 1):
-    AdaLN -> FP8 q/k/v -> RMSNorm+RoPE(q,k) -> window partition (2,8,8) ->
-    block-sparse attention -> reverse -> FP8 o -> gate_add -> AdaLN ->
-    FP8 GELU FFN -> gate_add (integrate.py:151-182 without cross-attention).
-    ``mod`` is [6, dim] = modulation + t_mod; params holds the quantised
-    weights: q,k,v,o,ffn0,ffn2 as (codes, scale, bias) and norm_q/norm_k.
-    ``cross`` (norm3_w, norm3_b, q, o, norm_q, k, v) adds the cross-attention
-    residual after the self-attention one (integrate.py:171)."""
-    f, h, w = fhw
-    L, dim = x.shape
-    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = [mod[i][None, None] for i in range(6)]
+              cross=None, per_token: bool = True, cache=None, kv_len=None,
+              return_cache: bool = False, windows=None, acc=np.float64):
+    """One DiT block on [L, dim] bf16 values (batch 1), integrate.py:151-182:
+    AdaLN -> self-attention (above) -> gate_add -> [x + cross-attention of
+    norm3(x)] -> AdaLN -> FP8 GELU FFN -> gate_add.
+    ``mod`` is [6, dim] = modulation + t_mod, split (shift, scale, gate) for
+    the attention then the FFN (integrate.py:154-155).  ``params`` holds the
+    quantised weights q, k, v, o, ffn0, ffn2 as (codes, scale, bias) and
+    norm_q / norm_k.  ``cross`` (norm3_w, norm3_b, q, o, norm_q, k, v) adds the
+    cross-attention residual (integrate.py:171).  ``per_token`` picks per-token
+    activation scales (else per tensor, the reference's default).
+    ``windows``: the output rows of those query windows' tokens only (in
+    window order; see self_attention).  With ``return_cache`` returns
+    (out, cache_k, cache_v)."""
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = \
+        [mod[i][None, None] for i in range(6)]
     xin = ln_modulate(x[None], scale_msa, shift_msa, eps)[0]
-    q = linear_fp8(xin, *params["q"])
-    k = linear_fp8(xin, *params["k"])
-    v = linear_fp8(xin, *params["v"])
-    q = rms_rope(q[None], params["norm_q"], cos, sin, eps)[0]
-    k = rms_rope(k[None], params["norm_k"], cos, sin, eps)[0]
-    qw = window_partition(q.reshape(1, f, h, w, dim)).reshape(-1, heads, dim // heads)
-    kw = window_partition(k.reshape(1, f, h, w, dim)).reshape(-1, heads, dim // heads)
-    vw = window_partition(v.reshape(1, f, h, w, dim)).reshape(-1, heads, dim // heads)
-    att = bf16(sparse_attention(qw, kw, vw, keep)).reshape(-1, 128, dim)
-    att = window_reverse(att, (f, h, w))[0]
-    o = linear_fp8(att, *params["o"])
+    o, ck, cv = self_attention(xin, params, fhw, keep, cos, sin, heads, eps, per_token, cache,
+                               kv_len, windows, acc)
+    if windows is not None:
+        x = np.asarray(x)[window_tokens(fhw, windows)]
     x = gate_add(x[None], gate_msa, o[None])[0]
     if cross is not None:
         x = cross_attention_block(x, cross["norm3_w"], cross["norm3_b"], cross["q"],
-                                  cross["norm_q"], cross["k"], cross["v"], cross["o"], heads, eps)
+                                  cross["norm_q"], cross["k"], cross["v"], cross["o"], heads, eps,
+                                  per_token=per_token)
     xin = ln_modulate(x[None], scale_mlp, shift_mlp, eps)[0]
-    y = ffn_fp8(xin, *params["ffn0"], *params["ffn2"])
-    return gate_add(x[None], gate_mlp, y[None])[0]
+    y = ffn_fp8(xin, *params["ffn0"], *params["ffn2"], per_token=per_token, acc=acc)
+    out = gate_add(x[None], gate_mlp, y[None])[0]
+    return (out, ck, cv) if return_cache else out
