@@ -470,20 +470,31 @@ def dense_attention(q, k, v, sm_scale=None) -> np.ndarray:
     return out
 
 
+def _stage(teacher, name: str, value):
+    """The value a composition continues with after stage ``name``: the
+    oracle's own, or what ``teacher(name, value)`` returns (a test hands back
+    the device's value of that stage after comparing the two, so each stage
+    is checked on exactly the device's input to it)."""
+    return value if teacher is None else teacher(name, value)
+
+
 def cross_attention_block(x, norm3_w, norm3_b, params_q, norm_q_w, cache_k, cache_v, params_o,
-                          heads: int = 12, eps: float = 1e-6, per_token: bool = True):
+                          heads: int = 12, eps: float = 1e-6, per_token: bool = True,
+                          teacher=None):
     """x + cross_attn(norm3(x)) on [L, dim] bf16 values (integrate.py:132-143,171):
     LayerNorm(affine) -> FP8 q -> RMSNorm (no RoPE) -> dense attention over the
-    cached K/V [Lk, dim] -> FP8 o -> residual add in bf16."""
+    cached K/V [Lk, dim] -> FP8 o -> residual add in bf16.  Stages: norm3,
+    cross_q, cross_q_rms, cross_attn, cross_o, cross_res."""
     L, dim = x.shape
-    xin = layer_norm_affine(x, norm3_w, norm3_b, eps)
-    q = linear_fp8(xin, *params_q, per_token=per_token)
-    q = rms_rope(q[None], norm_q_w, eps=eps, rope=False)[0]
+    xin = _stage(teacher, "norm3", layer_norm_affine(x, norm3_w, norm3_b, eps))
+    q = _stage(teacher, "cross_q", linear_fp8(xin, *params_q, per_token=per_token))
+    q = _stage(teacher, "cross_q_rms", rms_rope(q[None], norm_q_w, eps=eps, rope=False)[0])
     hd = dim // heads
     att = bf16(dense_attention(q.reshape(L, heads, hd), np.asarray(cache_k).reshape(-1, heads, hd),
                                np.asarray(cache_v).reshape(-1, heads, hd)).astype(np.float32))
-    o = linear_fp8(att.reshape(L, dim), *params_o, per_token=per_token)
-    return bf16(np.asarray(x, np.float32) + o)
+    att = _stage(teacher, "cross_attn", att.reshape(L, dim))
+    o = _stage(teacher, "cross_o", linear_fp8(att, *params_o, per_token=per_token))
+    return _stage(teacher, "cross_res", bf16(np.asarray(x, np.float32) + o))
 
 
 # ----------------------------------------------------------------------------
@@ -521,7 +532,7 @@ def ffn_fp8(x: np.ndarray, w1q, w1s, b1, w2q, w2s, b2, per_token: bool = True,
 
 def self_attention(xin, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6,
                    per_token: bool = True, cache=None, kv_len=None, windows=None,
-                   acc=np.float64):
+                   acc=np.float64, teacher=None):
     """The DiT self-attention (integrate.py:47-124) on [L, dim] bf16 values:
     FP8 q/k/v -> RMSNorm+RoPE(q, k) -> window partition (2,8,8) -> cached
     windows in front of k and v -> block-sparse attention (kept blocks
@@ -532,17 +543,20 @@ def self_attention(xin, params, fhw, keep, cos, sin, heads: int = 12, eps: float
     ``windows`` (per-token scales only, where rows are independent outside
     the attention): evaluate q, the attention and o only for the tokens of
     these query windows; o then holds those tokens' rows, in window order.
-    Returns (o, cache_k, cache_v)."""
+    Stages (``teacher``, whole-sequence evaluation only): q_proj, k_proj,
+    v_proj, q_rope, k_rope ([L, dim] raster order), attn (window order),
+    o_proj.  Returns (o, cache_k, cache_v)."""
     f, h, w = fhw
     L, dim = xin.shape
     hd = dim // heads
-    k, v = (linear_fp8(xin, *params[n], per_token=per_token, acc=acc) for n in ("k", "v"))
-    k = rms_rope(k[None], params["norm_k"], cos, sin, eps)[0]
+    k, v = (_stage(teacher, n + "_proj", linear_fp8(xin, *params[n], per_token=per_token,
+                                                    acc=acc)) for n in ("k", "v"))
+    k = _stage(teacher, "k_rope", rms_rope(k[None], params["norm_k"], cos, sin, eps)[0])
     kw, vw = (window_partition(t.reshape(1, f, h, w, dim)) for t in (k, v))
     if windows is None:
-        q = linear_fp8(xin, *params["q"], per_token=per_token, acc=acc)
-        qw = window_partition(rms_rope(q[None], params["norm_q"], cos, sin, eps)[0]
-                              .reshape(1, f, h, w, dim))
+        q = _stage(teacher, "q_proj", linear_fp8(xin, *params["q"], per_token=per_token, acc=acc))
+        q = _stage(teacher, "q_rope", rms_rope(q[None], params["norm_q"], cos, sin, eps)[0])
+        qw = window_partition(q.reshape(1, f, h, w, dim))
         qkeep = keep
     else:
         assert per_token, "a window subset needs row-local (per-token) quantisation"
@@ -557,11 +571,10 @@ def self_attention(xin, params, fhw, keep, cos, sin, heads: int = 12, eps: float
         vw = np.concatenate([cache[1], vw])
     att = bf16(sparse_attention(qw.reshape(-1, heads, hd), kw.reshape(-1, heads, hd),
                                 vw.reshape(-1, heads, hd), qkeep))
+    att = _stage(teacher, "attn", att.reshape(-1, dim))
     if windows is None:
         att = window_reverse(att.reshape(-1, 128, dim), (f, h, w))[0]
-    else:
-        att = att.reshape(-1, dim)
-    o = linear_fp8(att, *params["o"], per_token=per_token, acc=acc)
+    o = _stage(teacher, "o_proj", linear_fp8(att, *params["o"], per_token=per_token, acc=acc))
     if kv_len is not None and kw.shape[0] // per_step > kv_len:
         kw, vw = kw[per_step:], vw[per_step:]
     return o, kw, vw
@@ -576,7 +589,7 @@ def window_tokens(fhw, windows) -> np.ndarray:
 
 def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float = 1e-6,
               cross=None, per_token: bool = True, cache=None, kv_len=None,
-              return_cache: bool = False, windows=None, acc=np.float64):
+              return_cache: bool = False, windows=None, acc=np.float64, teacher=None):
     """One DiT block on [L, dim] bf16 values (batch 1), integrate.py:151-182:
     AdaLN -> self-attention (above) -> gate_add -> [x + cross-attention of
     norm3(x)] -> AdaLN -> FP8 GELU FFN -> gate_add.
@@ -587,21 +600,24 @@ def dit_block(x, mod, params, fhw, keep, cos, sin, heads: int = 12, eps: float =
     cross-attention residual (integrate.py:171).  ``per_token`` picks per-token
     activation scales (else per tensor, the reference's default).
     ``windows``: the output rows of those query windows' tokens only (in
-    window order; see self_attention).  With ``return_cache`` returns
-    (out, cache_k, cache_v)."""
+    window order; see self_attention).  ``teacher(name, value)``, if given,
+    is called with each stage's value and returns the one to continue with
+    (stages ln1, the self-attention's, gate1, the cross-attention's, ln2, ffn,
+    out).  With ``return_cache`` returns (out, cache_k, cache_v)."""
     shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, gate_mlp = \
         [mod[i][None, None] for i in range(6)]
-    xin = ln_modulate(x[None], scale_msa, shift_msa, eps)[0]
+    xin = _stage(teacher, "ln1", ln_modulate(x[None], scale_msa, shift_msa, eps)[0])
     o, ck, cv = self_attention(xin, params, fhw, keep, cos, sin, heads, eps, per_token, cache,
-                               kv_len, windows, acc)
+                               kv_len, windows, acc, teacher)
     if windows is not None:
         x = np.asarray(x)[window_tokens(fhw, windows)]
-    x = gate_add(x[None], gate_msa, o[None])[0]
+    x = _stage(teacher, "gate1", gate_add(x[None], gate_msa, o[None])[0])
     if cross is not None:
         x = cross_attention_block(x, cross["norm3_w"], cross["norm3_b"], cross["q"],
                                   cross["norm_q"], cross["k"], cross["v"], cross["o"], heads, eps,
-                                  per_token=per_token)
-    xin = ln_modulate(x[None], scale_mlp, shift_mlp, eps)[0]
-    y = ffn_fp8(xin, *params["ffn0"], *params["ffn2"], per_token=per_token, acc=acc)
-    out = gate_add(x[None], gate_mlp, y[None])[0]
+                                  per_token=per_token, teacher=teacher)
+    xin = _stage(teacher, "ln2", ln_modulate(x[None], scale_mlp, shift_mlp, eps)[0])
+    y = _stage(teacher, "ffn", ffn_fp8(xin, *params["ffn0"], *params["ffn2"],
+                                        per_token=per_token, acc=acc))
+    out = _stage(teacher, "out", gate_add(x[None], gate_mlp, y[None])[0])
     return (out, ck, cv) if return_cache else out
