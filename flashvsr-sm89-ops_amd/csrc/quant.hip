@@ -16,6 +16,9 @@
 // results, generated at build time from the operation sequence of
 // gelu_tanh_bf16 (csrc/gelu_table_gen.c), sit in every workgroup's LDS.
 #pragma clang fp contract(off)
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -604,6 +607,71 @@ extern "C" int fvsr_quant_weight_fp8(const void* w, int64_t n, int64_t k, int mo
   hipLaunchKernelGGL(quant_weight_tensor, dim3(P), dim3(kThreads), 0, st, wp, n, k, workspace, P,
                      qp, scale_out);
   return fvsr_launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant of fvsr_quant_fp8, for callers that cannot allocate
+// (code under stream capture, serving loops).  The per-tensor partial maxima
+// live in a file-scope device array instead of a caller workspace.  Each GPU
+// holds its own copy of the array at its own address, resolved once per device
+// by hipGetSymbolAddress with that device current; host code passes only that
+// resolved address to kernels, never the array's name (a host-side stand-in).
+// Calls that overlap on one GPU share the array and race.
+// ---------------------------------------------------------------------------
+constexpr int kScratchFloats = kMaxPartials;  // 4 KiB per GPU
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on device `dev`.
+int scratch_on(int dev, float** out) {
+  if (dev < 0 || dev >= kMaxDevices) return FVSR_EUNSUPPORTED;
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      int cur = 0;
+      if (hipGetDevice(&cur) != hipSuccess) return FVSR_EHIP;
+      if (cur != dev && hipSetDevice(dev) != hipSuccess) return FVSR_EHIP;
+      void* addr = nullptr;
+      const hipError_t e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (cur != dev && hipSetDevice(cur) != hipSuccess) return FVSR_EHIP;
+      if (e != hipSuccess || addr == nullptr) return FVSR_EHIP;
+      p = (float*)addr;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return FVSR_OK;
+}
+}  // namespace
+
+extern "C" int fvsr_quant_fp8_noalloc(const void* x, int64_t rows, int64_t cols, int64_t ld,
+                                      int mode, int gelu, void* codes, float* scale_out,
+                                      void* stream) {
+  if (rows < 0 || cols < 0 || ld < cols || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW))
+    return FVSR_EINVAL;
+  if (rows == 0 || cols == 0) return FVSR_OK;
+  if (!x || !codes || !scale_out) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xp = (const uint16_t*)x;
+  uint8_t* qp = (uint8_t*)codes;
+  if (mode == FVSR_SCALE_ROW)
+    return gelu ? launch_rows<true>(xp, rows, cols, ld, qp, scale_out, st)
+                : launch_rows<false>(xp, rows, cols, ld, qp, scale_out, st);
+  if (partial_blocks(rows) > kScratchFloats) return FVSR_EWORKSPACE;
+  int dev = 0;
+  if ((st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev)) != hipSuccess) return FVSR_EHIP;
+  float* ws = nullptr;
+  const int rc = scratch_on(dev, &ws);
+  if (rc != FVSR_OK) return rc;
+  // every partial the second pass reads is written by the first: nothing to clear
+  return gelu ? launch_tensor<true>(xp, rows, cols, ld, qp, scale_out, ws, st)
+              : launch_tensor<false>(xp, rows, cols, ld, qp, scale_out, ws, st);
 }
 
 extern "C" const char* fvsr_version(void) { return "fvsr 0.1.0 gfx950"; }

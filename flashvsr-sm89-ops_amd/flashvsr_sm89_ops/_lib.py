@@ -36,6 +36,7 @@ _SIGS = {
     "fvsr_version": ([], ctypes.c_char_p),
     "fvsr_quant_workspace_floats": ([_I64, _I64, _I], _I64),
     "fvsr_quant_fp8": ([_P, _I64, _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
+    "fvsr_quant_fp8_noalloc": ([_P, _I64, _I64, _I64, _I, _I, _P, _P, _P], _I),
     "fvsr_gelu_quant_fp8_tensor": ([_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P], _I),
     "fvsr_quant_weight_fp8": ([_P, _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
     "fvsr_fp8_gemm": ([_P, _I64, _P, _I, _P, _I64, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I,

@@ -70,6 +70,20 @@ int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mo
                    void* stream);
 
 /*
+ * fvsr_quant_fp8 without a workspace argument: no counterpart in the
+ * reference; for callers that cannot allocate (code under stream capture,
+ * tight serving loops, harnesses that forbid allocation).  Same arguments,
+ * codes and scales as fvsr_quant_fp8.  The per-tensor partial maxima live in a
+ * library-owned device array of 1024 floats per GPU (every size fits: the
+ * per-tensor pass uses at most 1024 partials; FVSR_EWORKSPACE otherwise),
+ * resolved on the first call on each device.  Nothing is allocated.  Calls
+ * that overlap on one GPU (two streams at once) share that array and race;
+ * serialise them.
+ */
+int fvsr_quant_fp8_noalloc(const void* x, int64_t rows, int64_t cols, int64_t ld, int mode,
+                           int gelu, void* codes, float* scale_out, void* stream);
+
+/*
  * Per-tensor e4m3 quantisation of tanh-GELU(h), the FFN mid-section of FP8FFN
  * (fp8_ffn.py:43-72,84-96) in the reference's per-tensor mode, after an
  * FVSR_EPI_ROWMAX GEMM: h bf16 [rows, cols] contiguous, hmax_part float
