@@ -16,8 +16,14 @@ Alongside it the JSON line carries
   components    op-level measurements at the other BASELINE configs
                 (C1 FP8 linear, C2 RMSNorm+RoPE, C3 AdaLN + FP8 FFN, C4 BSA),
                 inputs rotated over > 512 MB so the 256 MB MALL cannot serve them;
-  cpu_baseline  the CPU oracle (numpy + C) running one DiT block of the same
-                workload on this machine's host cores.
+  cpu_baseline  the reference path's PyTorch eager chain (oracle/eager.py)
+                running one DiT block of the same workload on this machine's
+                host cores.
+
+    python bench.py --blaslt          torch._scaled_mm (hipBLASLt) at the same
+                                      GEMM shapes, for comparison
+    python bench.py --mfma-from CSV   MFMA utilisation from a rocprofv3 --pmc
+                                      run over the MFMA counters
 """
 from __future__ import annotations
 
@@ -230,18 +236,25 @@ def components(torch, fv):
     b1 = torch.zeros(FFN, dtype=torch.bfloat16, device=dev)
     b2 = torch.zeros(DIM, dtype=torch.bfloat16, device=dev)
     lin1 = SimpleNamespace(weight=w1, w_scale=s1, bias=b1)
-    x8s = [fv.fused_ln_modulate_quant(x, sc, sh) for x in xs[:2]]
+    # GEMM inputs rotated past the MALL: ffn0 reads 26 MB of codes per call
+    # (its 303 MB output alone exceeds the MALL), ffn2 151 MB.
+    x8s = [fv.fused_ln_modulate_quant(xs[i % ns], sc, sh) for i in range(n_sets_for(M3 * DIM))]
+    nx = len(x8s)
     hb = torch.empty((M3, FFN), dtype=torch.bfloat16, device=dev)
-    t_g1 = timeit(torch, lambda i: fv.fp8_gemm(x8s[i % 2][0], x8s[i % 2][1], w1, s1, b1, out=hb), 2)
-    hs_ = [fv.fp8_gemm(x8s[i][0], x8s[i][1], w1, s1, b1) for i in range(2)]
-    t_rq = timeit(torch, lambda i: fv.fused_gelu_quant_fp8(hs_[i % 2], per_token=True), 2)
+    t_g1 = timeit(torch, lambda i: fv.fp8_gemm(x8s[i % nx][0], x8s[i % nx][1], w1, s1, b1, out=hb), nx)
+    nh = n_sets_for(M3 * FFN * 2)
+    hs_ = [fv.fp8_gemm(x8s[i % nx][0], x8s[i % nx][1], w1, s1, b1) for i in range(nh)]
+    t_rq = timeit(torch, lambda i: fv.fused_gelu_quant_fp8(hs_[i % nh], per_token=True), nh)
     rq_bytes = M3 * FFN * 3 + M3 * 4
-    hq, hsc = fv.fused_gelu_quant_fp8(hs_[0], per_token=True)
+    hqs = [fv.fused_gelu_quant_fp8(hs_[i], per_token=True) for i in range(min(nh, 5))]
+    del hs_
+    nq = len(hqs)
     res = xs[0].view(M3, DIM)
     o2 = torch.empty((M3, DIM), dtype=torch.bfloat16, device=dev)
-    t_g2 = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2), 1)
-    t_g2g = timeit(torch, lambda i: fv.fp8_gemm(hq, hsc, w2, s2, b2, out=o2, epilogue=_lib.EPI_GATE_ADD,
-                                                res=res, gate=gt.view(DIM)), 1)
+    t_g2 = timeit(torch, lambda i: fv.fp8_gemm(hqs[i % nq][0], hqs[i % nq][1], w2, s2, b2, out=o2), nq)
+    t_g2g = timeit(torch, lambda i: fv.fp8_gemm(hqs[i % nq][0], hqs[i % nq][1], w2, s2, b2, out=o2,
+                                                epilogue=_lib.EPI_GATE_ADD, res=res,
+                                                gate=gt.view(DIM)), nq)
     t_ga = timeit(torch, lambda i: fv.fused_gate_add(xs[i], gt, xs[(i + 1) % ns]), ns)
     ga_bytes = M3 * DIM * 6 + DIM * 2
     from flashvsr_sm89_ops.fused_adaln import fused_gate_add_ln_modulate_quant
@@ -249,7 +262,7 @@ def components(torch, fv):
         xs[i], gt, xs[(i + 1) % ns], sc, sh), ns)
     gal_bytes = M3 * DIM * (2 + 2 + 2 + 1) + M3 * 4 + 4 * DIM * 2
     t_ffn = timeit(torch, lambda i: (lambda h8: fv.fp8_gemm(h8[0], h8[1], w2, s2, b2))(
-        gemm_gelu_quant_fp8(x8s[i % 2][0], x8s[i % 2][1], lin1, True)), 2)
+        gemm_gelu_quant_fp8(x8s[i % nx][0], x8s[i % nx][1], lin1, True)), nx)
     fl = 2 * M3 * DIM * FFN
     out["C3_adaln_fp8_ffn"] = {
         "ln_modulate_quant_ms": t_ln, "ln_modulate_quant_GBps": gbs(ln_bytes, t_ln),
@@ -267,26 +280,29 @@ def components(torch, fv):
         "gate_add_ln_modulate_quant_GBps": gbs(gal_bytes, t_gal),
         "gate_add_ln_modulate_quant_frac_hbm": gbs(gal_bytes, t_gal) * 1e9 / PEAK["hbm"],
         "ffn_chain_ms": t_ffn}
-    del xs, x8s, hs_, hq, hb
+    del xs, x8s, hqs, hb
 
-    # C4: block-sparse attention [1,12,16896,128], C4 mask, plus a density sweep.
-    qkv = [randn(1, HEADS, L, HD) for _ in range(3)]
+    # C4: block-sparse attention [1,12,16896,128], C4 mask, plus a density sweep;
+    # q/k/v rotated over 4 sets (623 MB > the 256 MB MALL).
+    ns4 = n_sets_for(3 * HEADS * L * HD * 2)
+    qkvs = [[randn(1, HEADS, L, HD) for _ in range(3)] for _ in range(ns4)]
+    qkv = qkvs[0]
     keep = window_plus_random_mask(device=dev)
     kept = int(keep.sum().item())
-    t4 = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkv, keep), 1, iters=10)
+    t4 = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkvs[i], keep), ns4, iters=12)
     fl4 = 4 * 128 ** 3 * kept
     sweep = []
     from flashvsr_sm89_ops.lcsa.masks import density_mask
     for d in (0.1, 0.2, 0.3, 0.5, 0.75, 1.0):
         km = density_mask(HEADS, 132, 132, d, seed=11, device=dev)
         kk = int(km.sum().item())
-        td = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkv, km), 1, iters=5)
+        td = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkvs[i], km), ns4, iters=8)
         sweep.append({"density": kk / (HEADS * 132 * 132), "ms": td,
                       "TFLOPs": 4 * 128 ** 3 * kk / (td * 1e-3) / 1e12})
-    out["C4_bsa"] = {"ms_per_layer": t4, "density": kept / (HEADS * 132 * 132),
+    out["C4_bsa"] = {"ms_per_layer": t4, "density": kept / (HEADS * 132 * 132), "input_sets": ns4,
                      "TFLOPs": fl4 / (t4 * 1e-3) / 1e12, "frac_bf16": fl4 / (t4 * 1e-3) / PEAK["bf16"],
                      "density_sweep": sweep}
-    del qkv
+    del qkv, qkvs
 
     # Draft block mask + block index at the C5 geometry: q, k raster [16896, 1536]
     # read through the window token map, local range 7 on the 6x11 block grid,
@@ -522,33 +538,58 @@ def enable_block_step(torch, fv, dev, per_token=True):
             "geometry": "f=2, 48x88 latent, 132-window cache, top-k 30% of 3 time rows"}
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(args):
-    """One DiT block of the C5 workload through the CPU oracle (numpy + C)."""
+    """One DiT block of the C5 workload as the reference's PyTorch eager chain
+    on the host cores (oracle/eager.py: F.layer_norm, eager e4m3 quantisation,
+    fp32 dequant matmuls, upstream RMSNorm + complex RoPE, the per-block
+    sparse attention loop, F.gelu) with the same weights' codes and the C4
+    block mask."""
     import numpy as np
+    import torch
     from oracle import oracle as O
+    from oracle.eager import dit_block_eager, q_weight
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    rng = np.random.default_rng(0)
-    x = O.bf16(rng.standard_normal((L, DIM)).astype(np.float32))
-    mod = O.bf16((0.1 * rng.standard_normal((6, DIM))).astype(np.float32))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
 
     def lin(n, k):
-        w = O.bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
-        q, s = O.quantize_weight(w, per_channel=True)
-        return q, s, np.zeros(n, np.float32)
+        w8, s = q_weight((torch.randn(n, k, generator=g) * 0.02).to(torch.bfloat16), True)
+        return w8, s, torch.zeros(n, dtype=torch.bfloat16)
 
-    params = {"q": lin(DIM, DIM), "k": lin(DIM, DIM), "v": lin(DIM, DIM), "o": lin(DIM, DIM),
-              "ffn0": lin(FFN, DIM), "ffn2": lin(DIM, FFN),
-              "norm_q": np.ones(DIM, np.float32), "norm_k": np.ones(DIM, np.float32)}
+    P = {n: lin(DIM, DIM) for n in "qkvo"}
+    P["ffn0"], P["ffn2"] = lin(FFN, DIM), lin(DIM, FFN)
+    P["norm_q"] = P["norm_k"] = (1 + 0.1 * torch.randn(DIM, generator=g)).to(torch.bfloat16)
+    x = torch.randn(L, DIM, generator=g).to(torch.bfloat16)
+    mod = (0.1 * torch.randn(6, DIM, generator=g)).to(torch.bfloat16)
     cos, sin = O.wan_rope_cos_sin(F, H, W)
+    freqs = torch.complex(torch.from_numpy(cos), torch.from_numpy(sin)).to(torch.complex128)
     keep = O.c4_block_mask()
-    t0 = time.perf_counter()
-    y = O.dit_block(x, mod, params, (F, H, W), keep, cos, sin, HEADS)
-    dt = time.perf_counter() - t0
-    assert np.isfinite(y).all()
+    times = []
+    for _ in range(4):  # one warm-up, then the median of 3
+        t0 = time.perf_counter()
+        y, _, _ = dit_block_eager(x, mod, P, (F, H, W), keep, freqs, HEADS, 1e-6, True,
+                                  acc=torch.float32, sparse=True)
+        times.append(time.perf_counter() - t0)
+        assert torch.isfinite(y.float()).all()
+    dt = sorted(times[1:])[1]
     return {"value": dt * 1e3, "unit": "ms/layer", "cores": threads, "kind": "port",
-            "sample": "1 of the 30 DiT blocks of the C5 chunk (16896 tokens), CPU oracle "
-                      "(numpy float64 GEMM accumulation + C quantisation), wall time"}
+            "cpu": cpu_model(),
+            "sample": "1 of the 30 DiT blocks of the C5 chunk (16896 tokens, C4 mask ~30%): the "
+                      "reference path's PyTorch eager chain (oracle/eager.py, fp32 dequant "
+                      "matmuls, per-block sparse attention); one warm-up, median of 3 wall "
+                      "times on the host cores"}
 
 
 def main():
@@ -565,9 +606,17 @@ def main():
     ap.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="summarise two rocprofv3 --pmc counter_collection.csv files "
                          "(FETCH_SIZE, WRITE_SIZE) of a --copy-probe-mib run into JSON and exit")
+    ap.add_argument("--mfma-from", metavar="CSV",
+                    help="summarise a rocprofv3 --pmc counter_collection.csv of the MFMA "
+                         "counters (" + " ".join(MFMA_COUNTERS) + ") into JSON and exit")
+    ap.add_argument("--blaslt", action="store_true",
+                    help="time torch._scaled_mm (hipBLASLt) at the BASELINE GEMM shapes and exit")
     args = ap.parse_args()
     if args.traffic_from:
         print(json.dumps(summarize_traffic(*args.traffic_from, args.copy_probe_mib), indent=1))
+        return
+    if args.mfma_from:
+        print(json.dumps(summarize_mfma(args.mfma_from), indent=1))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this operator pack runs on one GPU; multi-GPU runs are not part of "
@@ -579,6 +628,10 @@ def main():
     from flashvsr_sm89_ops import _lib
 
     log(f"{_lib.version()} on {torch.cuda.get_device_name(0)}")
+    if args.blaslt:
+        for r in blaslt_same_box(torch):
+            print(json.dumps(r), flush=True)
+        return
     if args.copy_probe_mib:
         n = args.copy_probe_mib * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
@@ -653,6 +706,71 @@ def summarize_traffic(fetch_csv, write_csv, copy_mib):
         out[op] = {"kernel": keys[0][0][:120], "fetch_bytes": fb, "write_bytes": wb,
                    "traffic": fb + wb}
     return out
+
+
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F8",
+                 "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
+MFMA_KERNELS = {"gemm_fp8": "gemm_fp8", "bsa": "bsa_fwd_kernel"}
+
+
+def summarize_mfma(csv_path, simds=1024, xcds=8):
+    """MFMA utilisation per kernel from one rocprofv3 --pmc pass over
+    MFMA_COUNTERS: busy = SQ_VALU_MFMA_BUSY_CYCLES summed over the SIMDs,
+    divided by (GPU-active cycles x SIMDs); GRBM_GUI_ACTIVE in the file is the
+    sum over the XCDs, so one XCD's active cycles are that over ``xcds``.
+    MOPS x 512 = the flops the matrix cores executed, against 2MNK /
+    4*128^3*blocks; the clock implied by the active cycles and the dispatch's
+    duration is reported as a check of that reading."""
+    import csv
+    acc = {}
+    with open(csv_path) as fh:
+        for row in csv.DictReader(fh):
+            name = row["Kernel_Name"]
+            op = next((k for k, frag in MFMA_KERNELS.items() if frag in name), None)
+            if op is None:
+                continue
+            d = acc.setdefault((op, name[:100], row["Dispatch_Id"]), {})
+            d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+            d["ns"] = float(row["End_Timestamp"]) - float(row["Start_Timestamp"])
+    out = {}
+    for (op, name, _), d in acc.items():
+        e = out.setdefault(op + " | " + name, {"dispatches": 0, "busy": 0.0, "active": 0.0,
+                                                "mops_f8": 0.0, "mops_bf16": 0.0, "ns": 0.0})
+        e["dispatches"] += 1
+        e["busy"] += d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        e["active"] += d.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+        e["mops_f8"] += d.get("SQ_INSTS_VALU_MFMA_MOPS_F8", 0.0)
+        e["mops_bf16"] += d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+        e["ns"] += d["ns"]
+    res = {}
+    for k, e in out.items():
+        n = e["dispatches"]
+        res[k] = {"dispatches": n, "mfma_busy_frac": e["busy"] / (e["active"] * simds),
+                  "mfma_flop_per_dispatch": (e["mops_f8"] + e["mops_bf16"]) * 512 / n,
+                  "avg_us": e["ns"] / n / 1e3, "implied_GHz": e["active"] / e["ns"]}
+    return res
+
+
+def blaslt_same_box(torch):
+    """torch._scaled_mm (hipBLASLt) at the BASELINE GEMM shapes on this GPU,
+    per-tensor and row-wise scales, for comparison with fvsr_fp8_gemm."""
+    dev = "cuda"
+    rows = []
+    for (M, N, K) in [(4224, 1536, 1536), (16896, 4608, 1536), (16896, 1536, 1536),
+                      (16896, 8960, 1536), (16896, 1536, 8960), (8192, 8192, 8192)]:
+        a = torch.randint(-100, 100, (M, K), device=dev).to(torch.float8_e4m3fn)
+        b = torch.randint(-100, 100, (N, K), device=dev).to(torch.float8_e4m3fn)
+        for mode in ("tensor", "row"):
+            if mode == "tensor":
+                sa, sb = torch.ones((), device=dev), torch.ones((), device=dev)
+            else:
+                sa, sb = torch.ones((M, 1), device=dev), torch.ones((1, N), device=dev)
+            t = timeit(torch, lambda i: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb,
+                                                         out_dtype=torch.bfloat16), 1, iters=20)
+            rows.append({"M": M, "N": N, "K": K, "scales": mode, "us": t * 1e3,
+                         "TFLOPs": 2 * M * N * K / (t * 1e-3) / 1e12})
+        del a, b
+    return rows
 
 
 def load_traffic(op):

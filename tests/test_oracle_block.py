@@ -3,39 +3,28 @@ closed form, and one DiT block (oracle.dit_block with oracle.self_attention,
 oracle.cross_attention_block and oracle.ffn_fp8) against a torch-eager block
 written from the reference's block (integrate.py:151-182, with the
 self-attention of :47-124 and the cross-attention of :132-143) out of torch's
-own operators: F.layer_norm, the reference's eager e4m3 quantisation
-expressions, dequantised matmuls, the upstream RMSNorm and float64 complex
-RoPE, scaled_dot_product_attention under the expanded block mask,
-F.gelu(approximate='tanh').  A slip in the oracle's composition (modulation
+own operators (oracle/eager.py): F.layer_norm, the reference's eager e4m3
+quantisation expressions, dequantised matmuls, the upstream RMSNorm and
+float64 complex RoPE, scaled_dot_product_attention under the expanded block
+mask, F.gelu(approximate='tanh').  A slip in the oracle's composition (modulation
 chunk order, (scale, shift) swapped, a residual dropped, the cache trimmed
 from the wrong end, a transposed window) fails these tests by far more than
 the tolerance, which only absorbs FP8 codes flipped by last-bit differences.
 """
-import math
-
 import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
 
 from oracle import oracle as O
+from oracle.eager import (attention_blocks, attention_dense, closed_form_window_of,
+                          dit_block_eager, modulate, q_weight)
 
 BF = torch.bfloat16
 E4M3 = torch.float8_e4m3fn
 
 
 # ----------------------------------------------------------------------------- window permutation
-
-def closed_form_window_of(B, f, h, w):
-    """(window, slot) of every token (b, t, r, c) by the closed form of a
-    (2, 8, 8) window partition: windows ordered (b, t//2, r//8, c//8), slots
-    (t%2, r%8, c%8)."""
-    b, t, r, c = np.meshgrid(np.arange(B), np.arange(f), np.arange(h), np.arange(w), indexing="ij")
-    per_b = (f // 2) * (h // 8) * (w // 8)
-    win = b * per_b + ((t // 2) * (h // 8) + r // 8) * (w // 8) + c // 8
-    slot = ((t % 2) * 8 + r % 8) * 8 + c % 8
-    return win, slot
-
 
 @pytest.mark.parametrize("B,f,h,w", [(1, 2, 8, 8), (1, 4, 16, 24), (2, 6, 8, 16)])
 def test_window_partition_closed_form(B, f, h, w):
@@ -56,104 +45,6 @@ def test_window_partition_closed_form(B, f, h, w):
 
 
 # ----------------------------------------------------------------------------- torch-eager block
-
-def q_act(x, per_token):
-    """Activation quantisation (fp8_quant.py:26-35,54; per row for per-token):
-    s = max(amax, 1e-12)/448, e4m3(clamp(x/s, +-448)), returned scale amax/448."""
-    xf = x.float()
-    amax = xf.abs().amax(dim=1, keepdim=True) if per_token else xf.abs().amax().reshape(1, 1)
-    s = amax.clamp(min=1e-12) / 448.0
-    return (xf / s).clamp(-448.0, 448.0).to(E4M3), amax / 448.0
-
-
-def q_weight(w, per_channel):
-    """FP8Linear.__init__ (fp8_linear.py:20-22) as eager torch evaluates it on a
-    bf16 weight; per channel the [N, 1] fp32 scale promotes w/s to fp32."""
-    if per_channel:
-        s = (w.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12).float()
-    else:
-        s = (w.abs().amax() / 448.0).clamp(min=1e-12).float()
-    return (w / s).to(E4M3), s.reshape(-1)
-
-
-def linear_eager(x, lin, per_token):
-    """_scaled_mm(x8, W8.t(), s_x, s_w, bias) -> bf16 as a float64 dequant matmul."""
-    w8, sw, b = lin
-    x8, sx = q_act(x, per_token)
-    y = (x8.double() @ w8.double().T) * sx.double() * sw.double().reshape(1, -1)
-    return (y + b.double()).float().to(BF)
-
-
-def rms_norm_upstream(x, weight, eps):
-    """Wan RMSNorm: (x.float() * rsqrt(mean(x^2) + eps)).to(bf16) * weight."""
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(BF) * weight
-
-
-def rope_upstream(x, freqs, heads):
-    """Wan rope_apply: float64 complex product over interleaved pairs -> bf16."""
-    L, D = x.shape
-    xc = torch.view_as_complex(x.double().reshape(L, heads, -1, 2))
-    return torch.view_as_real(xc * freqs[:, None, :]).reshape(L, D).to(BF)
-
-
-def modulate(x, shift, scale):
-    return x * (1 + scale) + shift
-
-
-def attention_eager(q, k, v, keep_tokens, heads):
-    """Per head scaled_dot_product_attention in fp32 under a [Lq, Lk] bool mask."""
-    hd = q.shape[1] // heads
-    out = []
-    for h in range(heads):
-        sl = slice(h * hd, (h + 1) * hd)
-        m = keep_tokens[h] if keep_tokens is not None else None
-        out.append(F.scaled_dot_product_attention(q[None, :, sl].float(), k[None, :, sl].float(),
-                                                  v[None, :, sl].float(), attn_mask=m)[0])
-    return torch.cat(out, 1).to(BF)
-
-
-def window_order(f, h, w):
-    """raster token of each window position, from the closed form above."""
-    win, slot = closed_form_window_of(1, f, h, w)
-    tok = np.empty(f * h * w, np.int64)
-    tok[(win * 128 + slot).reshape(-1)] = np.arange(f * h * w)
-    return torch.from_numpy(tok)
-
-
-def dit_block_eager(x, mod, P, fhw, keep, freqs, heads, eps, per_token, cross, cache, kv_len):
-    """The reference DiT block with its stock helpers, eager torch on bf16 CPU tensors."""
-    f, h, w = fhw
-    L, D = x.shape
-    sh_a, sc_a, g_a, sh_f, sc_f, g_f = mod.chunk(6, dim=0)
-    xin = modulate(F.layer_norm(x, (D,), eps=eps), sh_a, sc_a)
-    q = rope_upstream(rms_norm_upstream(linear_eager(xin, P["q"], per_token), P["norm_q"], eps),
-                      freqs, heads)
-    k = rope_upstream(rms_norm_upstream(linear_eager(xin, P["k"], per_token), P["norm_k"], eps),
-                      freqs, heads)
-    v = linear_eager(xin, P["v"], per_token)
-    tok = window_order(f, h, w)
-    q_w, k_w, v_w = q[tok], k[tok], v[tok]                        # window order
-    per_step = (L // 128) // (f // 2)
-    if cache is not None:
-        k_w = torch.cat([cache[0], k_w])
-        v_w = torch.cat([cache[1], v_w])
-    km = torch.from_numpy(keep).repeat_interleave(128, 1).repeat_interleave(128, 2)
-    att_w = attention_eager(q_w, k_w, v_w, km, heads)
-    att = torch.empty_like(att_w)
-    att[tok] = att_w
-    x = x + g_a * linear_eager(att, P["o"], per_token)
-    if k_w.shape[0] // 128 // per_step > kv_len:
-        k_w, v_w = k_w[per_step * 128:], v_w[per_step * 128:]
-    if cross is not None:
-        n3 = F.layer_norm(x, (D,), cross["norm3_w"], cross["norm3_b"], eps)
-        cq = rms_norm_upstream(linear_eager(n3, cross["q"], per_token), cross["norm_q"], eps)
-        x = x + linear_eager(attention_eager(cq, cross["k"], cross["v"], None, heads), cross["o"],
-                             per_token)
-    hmid = linear_eager(modulate(F.layer_norm(x, (D,), eps=eps), sh_f, sc_f), P["ffn0"], per_token)
-    y = linear_eager(F.gelu(hmid, approximate="tanh"), P["ffn2"], per_token)
-    return x + g_f * y, k_w, v_w
-
 
 def _np_lin(lin):
     w8, s, b = lin
@@ -294,3 +185,19 @@ def test_dit_block_window_subset_equals_full(with_cross):
     assert np.array_equal(tok[:128], want.reshape(-1))
     sub = O.dit_block(x, mod, P, fhw, keep, cos, sin, heads, cross=cross, windows=wins)
     assert np.array_equal(sub, full[tok])
+
+
+def test_eager_block_attention_matches_dense_sdpa():
+    """oracle.eager.attention_blocks (the per-block loop bench.py's CPU
+    baseline runs at full size) equals SDPA under the expanded mask."""
+    g = torch.Generator().manual_seed(9)
+    heads, NQ, NK = 2, 3, 5
+    q = torch.randn(NQ * 128, heads * 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(NK * 128, heads * 128, generator=g).to(torch.bfloat16)
+    v = torch.randn(NK * 128, heads * 128, generator=g).to(torch.bfloat16)
+    keep = O.random_block_mask(heads, NQ, NK, 0.5, seed=3)
+    km = torch.from_numpy(keep).repeat_interleave(128, 1).repeat_interleave(128, 2)
+    a = attention_blocks(q, k, v, keep, heads).float()
+    b = attention_dense(q, k, v, km, heads).float()
+    assert (a - b).abs().max() <= 1.6e-2          # both rounded to bf16 once
+    assert (a == b).float().mean() > 0.95
