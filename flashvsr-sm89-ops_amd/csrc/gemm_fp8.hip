@@ -9,20 +9,15 @@
 // side and the activation as the "B" side, so each lane's accumulators hold 4
 // consecutive output columns of one output row.
 //
-// Main loop (K a multiple of 64): a 4-slot LDS ring of 64-wide K steps
-// (32 KB per slot: 256 A rows + 256 B rows of 64 bytes).  Operand tiles go
-// from global memory straight into LDS (global_load_lds_dwordx4, no staging
-// registers) three steps ahead of the MFMAs; each wave reads the MFMA
-// fragments of step k+1 from LDS while the MFMAs of step k run.  The four slots
-// are four distinct LDS objects and the loop is unrolled by four, so the
-// compiler can see that the reads of one slot never alias the loads into
-// another and does not serialise them.  Rows are 64 bytes = 4 chunks of 16;
-// chunk c of row r sits at c ^ ((r >> 2) & 3), which makes the 16 rows one
-// ds_read_b128 phase touches land on 16 distinct 16-byte bank groups.
-// Other K (a multiple of 16) use a register-staged loop with K step 128.
+// Main loop (K a multiple of 256, at least 512): a persistent kernel, one
+// workgroup per CU, streaming K through two 64 KB LDS pair slots (128 bytes
+// of K for the 256 A rows and 256 B rows) filled by buffer_load ... lds
+// straight from memory, one load per MFMA; the last K steps of a tile already
+// load the next tile's first pairs (details at gemm_fp8_ring).  Other K (a
+// multiple of 16) use a register-staged loop with K step 128.
 //
-// Epilogue: y = acc * sa[m] * sb[n] + bias[n] is written as bf16 into the (now
-// free) LDS as a 256 x 256 tile, then every thread stores 16-byte row chunks:
+// Epilogue: y = acc * (sa[m] * sb[n]) + bias[n], rounded to bf16, leaves
+// through a per-wave LDS staging area as 16-byte row chunks:
 //   FVSR_EPI_BIAS      C = y
 //   FVSR_EPI_ROWMAX    C = y, plus max(C) over each row's 128-column slab
 //   FVSR_EPI_GATE_ADD  C = bf16(res + bf16(gate[n] * y))
@@ -36,6 +31,10 @@ typedef int i32x4_t __attribute__((ext_vector_type(4)));
 __device__ void fvsr_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds,
                                      int size, int voffset, int soffset, int offset, int aux)
     __asm("llvm.amdgcn.raw.buffer.load.lds");
+// Raw buffer store of 16 bytes at base + voffset + soffset; a store whose
+// voffset lies past the descriptor's byte count is dropped by the hardware.
+__device__ void fvsr_buffer_store_b128(u32x4_t data, i32x4_t rsrc, int voffset, int soffset,
+                                       int aux) __asm("llvm.amdgcn.raw.buffer.store.v4i32");
 
 namespace {
 
@@ -60,6 +59,7 @@ struct EpiArgs {
   int sa_row, sb_col;
   int vec_params;  // sb (per column) 16-byte aligned and bias 8-byte aligned
   int res_vec;     // gate-add: N, ldc multiples of 8 and res / c / gate 16-byte aligned
+  int direct;      // c 16-byte aligned, ldc % 8 == 0, (M + 256) * ldc * 2 below 2^32
 };
 
 FVSR_DEV void map_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
@@ -248,10 +248,11 @@ FVSR_DEV void dma_offsets(DmaOffs& o, int64_t m0, int64_t n0, int64_t M, int64_t
   }
 }
 
-// Raw buffer descriptor over `base` (stride 0, no range limit below 4 GB).
-FVSR_DEV i32x4_t make_rsrc(const void* base) {
+// Raw buffer descriptor over `base` (stride 0, range `bytes`; no range limit
+// below 4 GB by default).
+FVSR_DEV i32x4_t make_rsrc(const void* base, uint32_t bytes = 0xffffffffu) {
   const uint64_t p = (uint64_t)base;
-  return i32x4_t{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), -1, 0x00020000};
+  return i32x4_t{(int)(uint32_t)p, (int)(uint32_t)(p >> 32), (int)bytes, 0x00020000};
 }
 
 // Stream one pair (A and B bytes [k0, k0+128) of the tile's rows) into a pair
@@ -349,10 +350,10 @@ FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_
 // Per-wave epilogue area: 32 rows x 64 columns of bf16 staging (4 KB, one
 // eighth of the wave's 128 x 128 quadrant per pass; 8-byte units XOR-swizzled
 // with the row so that 16 lanes writing 16 rows cover all banks), then the
-// quadrant's epilogue parameters: sa of its 128 rows, sb and bias of its 128
-// columns (1.25 KB).
+// quadrant's epilogue parameters as fp32: sa of its 128 rows, sb and bias of
+// its 128 columns (1.5 KB).
 constexpr int kEpiStageBytes = 32 * 128;
-constexpr int kEpiWaveBytes = kEpiStageBytes + 128 * 4 + 128 * 4 + 128 * 2;
+constexpr int kEpiWaveBytes = kEpiStageBytes + 3 * 128 * 4;
 FVSR_DEV int epi_off(int row, int unit) { return row * 128 + ((unit ^ (row & 15)) << 3); }
 
 // This lane's share of the quadrant's parameters (rows / columns q*64 + lane),
@@ -370,19 +371,19 @@ FVSR_DEV void fetch_epi_params(EpiParamRegs& r, const EpiArgs& e, int64_t m0, in
     const int64_t mc = m < M ? m : M - 1, nc = n < N ? n : N - 1;
     r.sa[q] = e.sa[e.sa_row ? mc : 0];
     r.sb[q] = e.sb[e.sb_col ? nc : 0];
-    r.bias[q] = e.bias ? (uint32_t)e.bias[nc] : 0u;
+    r.bias[q] = e.bias ? (uint32_t)e.bias[nc] << 16 : 0u;
   }
 }
 
 FVSR_DEV void put_epi_params(const EpiParamRegs& r, uint8_t LDS_AS* prm, int lane) {
   float LDS_AS* sa_l = (float LDS_AS*)prm;
   float LDS_AS* sb_l = sa_l + 128;
-  uint16_t LDS_AS* bi_l = (uint16_t LDS_AS*)(sb_l + 128);
+  uint32_t LDS_AS* bi_l = (uint32_t LDS_AS*)(sb_l + 128);
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     sa_l[q * 64 + lane] = r.sa[q];
     sb_l[q * 64 + lane] = r.sb[q];
-    bi_l[q * 64 + lane] = (uint16_t)r.bias[q];
+    bi_l[q * 64 + lane] = r.bias[q];
   }
 }
 
@@ -392,7 +393,7 @@ FVSR_DEV void epi_stage(const v16f (&acc)[4][4], uint16_t LDS_AS* stg,
                         const uint8_t LDS_AS* prm, int lane, int ip, int j) {
   const float LDS_AS* sa_l = (const float LDS_AS*)prm;
   const float LDS_AS* sb_l = sa_l + 128;
-  const uint16_t LDS_AS* bi_l = (const uint16_t LDS_AS*)(sb_l + 128);
+  const float LDS_AS* bi_l = sb_l + 128;
   const int h = lane >> 5;
   const int row = lane & 31;
   const float sam = sa_l[j * 32 + row];
@@ -402,13 +403,10 @@ FVSR_DEV void epi_stage(const v16f (&acc)[4][4], uint16_t LDS_AS* stg,
     for (int g = 0; g < 4; ++g) {
       const int cl = (2 * ip + ii) * 32 + g * 8 + h * 4;
       const f32x4_t sb = *(const f32x4_t LDS_AS*)(sb_l + cl);
-      const u32x2_t bw = *(const u32x2_t LDS_AS*)(bi_l + cl);
+      const f32x4_t bw = *(const f32x4_t LDS_AS*)(bi_l + cl);
       float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float b = (r & 1) ? bf_hi(bw[r >> 1]) : bf_lo(bw[r >> 1]);
-        y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam * sb[r]) + b;
-      }
+      for (int r = 0; r < 4; ++r) y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam * sb[r]) + bw[r];
       *(u32x2_t LDS_AS*)((uint8_t LDS_AS*)stg + epi_off(row, ii * 8 + g * 2 + h)) =
           u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
     }
@@ -484,6 +482,121 @@ FVSR_DEV void epi_store(const uint16_t LDS_AS* stg, int64_t mw, int64_t nw, int6
   }
 }
 
+// Epilogue of tiles whose 256 columns all lie inside the output (bias and
+// row-max epilogues).  The same eight 32 x 64 passes (column half ip, row
+// block j) through the wave's staging area as epi_stage / epi_store, arranged
+// so that nothing waits on LDS per value: the column scales and biases of one
+// 64-column half are read into registers once (64 VGPRs), and the passes are
+// software-pipelined -- pass p's staged rows are read back as 16-byte row
+// chunks, pass p + 1 is converted and written over them, then pass p's chunks
+// are stored (8 lanes = one 128-byte row segment).  A wave's LDS accesses
+// execute in order, so the rewrite cannot overtake the reads.  Stores go
+// through a buffer descriptor spanning the M output rows: stores of rows past
+// M are dropped by its range check.
+struct FastParams {
+  f32x4_t sb[2][4], bias[2][4];
+};
+
+FVSR_DEV void fast_params(FastParams& fp, const uint8_t LDS_AS* prm, int ip, int h) {
+  const float LDS_AS* sb_l = (const float LDS_AS*)prm + 128;
+  const float LDS_AS* bi_l = sb_l + 128;
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int cl = (2 * ip + ii) * 32 + g * 8 + h * 4;
+      fp.sb[ii][g] = *(const f32x4_t LDS_AS*)(sb_l + cl);
+      fp.bias[ii][g] = *(const f32x4_t LDS_AS*)(bi_l + cl);
+    }
+}
+
+// Convert pass (ip, j) and write it to the staging area.
+FVSR_DEV void fast_stage(const v16f (&acc)[4][4], const FastParams& fp, float sam,
+                         uint16_t LDS_AS* stg, int ip, int j, int row, int h) {
+#pragma unroll
+  for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        y[r] = acc[2 * ip + ii][j][g * 4 + r] * (sam * fp.sb[ii][g][r]) + fp.bias[ii][g][r];
+      *(u32x2_t LDS_AS*)((uint8_t LDS_AS*)stg + epi_off(row, ii * 8 + g * 2 + h)) =
+          u32x2_t{pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3])};
+    }
+}
+
+// Read the staged pass back: row s * 8 + lane / 8, 16-byte chunk lane % 8.
+FVSR_DEV void fast_read(const uint16_t LDS_AS* stg, u32x4_t (&v)[4], int lane) {
+  const int c8 = lane & 7;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int r8 = s * 8 + (lane >> 3);
+    const u32x2_t lo = *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)stg + epi_off(r8, 2 * c8));
+    const u32x2_t hi =
+        *(const u32x2_t LDS_AS*)((const uint8_t LDS_AS*)stg + epi_off(r8, 2 * c8 + 1));
+    v[s] = u32x4_t{lo[0], lo[1], hi[0], hi[1]};
+  }
+}
+
+template <int EPI>
+FVSR_DEV void fast_store(const u32x4_t (&v)[4], float (&vmax)[4], i32x4_t rc, int voff,
+                         int64_t ldc, int ip, int j) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (EPI == FVSR_EPI_ROWMAX) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) vmax[s] = fmaxf(vmax[s], fmaxf(bf_lo(v[s][w]), bf_hi(v[s][w])));
+    }
+    fvsr_buffer_store_b128(v[s], rc, voff + (int)((j * 32 + s * 8) * ldc * 2 + ip * 128), 0, 0);
+  }
+}
+
+template <int EPI>
+FVSR_DEV void epi_fast(const v16f (&acc)[4][4], uint16_t LDS_AS* stg, const uint8_t LDS_AS* prm,
+                       int64_t mw, int64_t nw, int64_t M, const EpiArgs& e, i32x4_t rc,
+                       int lane) {
+  const float LDS_AS* sa_l = (const float LDS_AS*)prm;
+  const int h = lane >> 5, row = lane & 31;
+  float sam[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) sam[j] = sa_l[j * 32 + row];
+  // Store offset of row lane / 8, chunk lane % 8; each pass adds its row
+  // block, row group and column half (all in the offset the range check
+  // covers).
+  const int voff = (int)(((mw + (lane >> 3)) * e.ldc + nw + (lane & 7) * 8) * 2);
+  float vmax[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) vmax[j][s] = -__builtin_huge_valf();
+  FastParams fp;
+  fast_params(fp, prm, 0, h);
+  fast_stage(acc, fp, sam[0], stg, 0, 0, row, h);
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+    const int ip = p >> 2, j = p & 3;
+    u32x4_t v[4];
+    fast_read(stg, v, lane);
+    if (p == 3) fast_params(fp, prm, 1, h);
+    if (p < 7) fast_stage(acc, fp, sam[(p + 1) & 3], stg, (p + 1) >> 2, (p + 1) & 3, row, h);
+    fast_store<EPI>(v, vmax[j], rc, voff, e.ldc, ip, j);
+  }
+  if (EPI == FVSR_EPI_ROWMAX) {
+    // 8 lanes per row cover 64 columns per pass; both halves = the slab.
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        float v = vmax[j][s];
+#pragma unroll
+        for (int o = 4; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+        const int64_t m = mw + j * 32 + s * 8 + (lane >> 3);
+        if ((lane & 7) == 0 && m < M) e.amax_part[m * e.nparts + nw / 128] = v;
+      }
+  }
+}
+
 FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t& n0) {
   int tm, tn;
   map_tile(t, tiles_m, tiles_n, tm, tn);
@@ -502,7 +615,7 @@ FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t&
 // wave).  After a workgroup's last tile the same stream re-fetches that
 // tile's first pairs (harmless) and the workgroup drains its loads before it
 // exits.
-template <int EPI>
+template <int EPI, bool DIRECT>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
                    int64_t ldb, int64_t M, int64_t N, int64_t K, EpiArgs ep) {
@@ -568,10 +681,12 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
 
     // Epilogue (fa/fb now hold the next tile's step-0 fragments): eight
     // passes of 32 rows x 64 columns through the wave's own staging area.
-    {
-      const int el = lane_here();
-      const int64_t mw = m0 + wm * 128, nw = n0 + wn * 128;
-      put_epi_params(epr, prm, el);
+    const int el = lane_here();
+    const int64_t mw = m0 + wm * 128, nw = n0 + wn * 128;
+    put_epi_params(epr, prm, el);
+    if (DIRECT) {
+      epi_fast<EPI>(acc, stg, prm, mw, nw, M, ep, make_rsrc(ep.c, (uint32_t)(M * ep.ldc * 2)), el);
+    } else {
       float vmax[4][4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -700,9 +815,14 @@ void gemm_fp8_generic(const uint8_t* __restrict__ A, int64_t lda, const uint8_t*
 template <int EPI>
 void launch(bool ring, unsigned grid, hipStream_t st, const uint8_t* a, int64_t lda,
             const uint8_t* b, int64_t ldb, int64_t M, int64_t N, int64_t K, const EpiArgs& ep) {
-  if (ring)
-    hipLaunchKernelGGL(gemm_fp8_ring<EPI>, dim3(grid), dim3(kThreads), 0, st, a, lda, b, ldb, M, N,
-                       K, ep);
+  // The fast epilogue needs whole column tiles; gate-add keeps the general
+  // one, which loads its residual rows ahead of the stores.
+  if (ring && EPI != FVSR_EPI_GATE_ADD && ep.direct && N % BN == 0)
+    hipLaunchKernelGGL((gemm_fp8_ring<EPI, EPI != FVSR_EPI_GATE_ADD>), dim3(grid), dim3(kThreads),
+                       0, st, a, lda, b, ldb, M, N, K, ep);
+  else if (ring)
+    hipLaunchKernelGGL((gemm_fp8_ring<EPI, false>), dim3(grid), dim3(kThreads), 0, st, a, lda, b,
+                       ldb, M, N, K, ep);
   else
     hipLaunchKernelGGL(gemm_fp8_generic<EPI>, dim3(grid), dim3(kThreads), 0, st, a, lda, b, ldb,
                        M, N, K, ep);
@@ -744,9 +864,10 @@ extern "C" int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa
   const int vec_params = (!sb_col || ((uintptr_t)sb & 15) == 0) && ((uintptr_t)bias & 7) == 0;
   const int res_vec = epilogue == FVSR_EPI_GATE_ADD && N % 8 == 0 && ldc % 8 == 0 &&
                       ((((uintptr_t)res) | (uintptr_t)c | (uintptr_t)gate) & 15) == 0;
+  const int direct = ((uintptr_t)c & 15) == 0 && ldc % 8 == 0 && (M + BM) * ldc * 2 <= 0xffffffffLL;
   EpiArgs ep{sa, sb, (const uint16_t*)bias, (uint16_t*)c, ldc, amax_part,
              fvsr_gemm_amax_parts(N), (const uint16_t*)res, (const uint16_t*)gate,
-             sa_mode == FVSR_SCALE_ROW, sb_col, vec_params, res_vec};
+             sa_mode == FVSR_SCALE_ROW, sb_col, vec_params, res_vec, direct};
   hipStream_t st = (hipStream_t)stream;
   // Persistent ring: K a multiple of 256, at least 8 K steps, and every row
   // offset of either operand within 32 bits.

@@ -315,7 +315,8 @@ def test_gelu_tensor_quant_small_values(ops):
 
 @pytest.mark.parametrize("MNK", [(256, 256, 64), (300, 520, 192), (4224, 1536, 1536),
                                  (1000, 600, 8960), (64, 64, 320), (4400, 4700, 512),
-                                 (2100, 9000, 768), (600, 300, 1280)])
+                                 (2100, 9000, 768), (600, 300, 1280), (1300, 4608, 1024),
+                                 (700, 2048, 8960)])
 def test_fp8_gemm_ring_shapes(ops, MNK):
     """The main-loop variants across K-step counts (persistent ring for K a
     multiple of 256 and >= 512, register-staged loop otherwise), ragged M, N,
@@ -325,6 +326,30 @@ def test_fp8_gemm_ring_shapes(ops, MNK):
     y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(sa).to(DEV), codes_dev(b),
                      torch.from_numpy(sb).to(DEV), dev_bf16(bias))
     _close_bf16(host_f(y), O.fp8_gemm(a, sa, b, sb, O.from_bf16_bits(bias)))
+
+
+@pytest.mark.parametrize("epi", ["bias", "rowmax"])
+@pytest.mark.parametrize("MNK", [(4224, 1536, 1536), (77, 512, 512), (1000, 2560, 768)])
+def test_fp8_gemm_direct_epilogue_rows_past_m(ops, MNK, epi):
+    """Whole column tiles store straight from the accumulators, with rows past
+    M dropped by the store descriptor's byte range: the output is a view of the
+    first M rows of a larger buffer whose remaining rows must keep a sentinel."""
+    from flashvsr_sm89_ops import _lib
+    M, N, K = MNK
+    a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=11 * M + N)
+    buf = torch.full((M + 300, N), 7.0, dtype=torch.bfloat16, device=DEV)
+    hmax = torch.empty((M, N // 128), dtype=torch.float32, device=DEV)
+    kw = dict(epilogue=_lib.EPI_ROWMAX, amax_part=hmax) if epi == "rowmax" else {}
+    y = ops.fp8_gemm(codes_dev(a), torch.from_numpy(sa).to(DEV), codes_dev(b),
+                     torch.from_numpy(sb).to(DEV), dev_bf16(bias), out=buf[:M], **kw)
+    assert y.data_ptr() == buf.data_ptr()
+    assert bool((buf[M:] == 7.0).all()), "a store landed past row M"
+    _close_bf16(host_f(y), O.fp8_gemm(a, sa, b, sb, O.from_bf16_bits(bias)))
+    if epi == "rowmax":
+        hf = O.from_bf16_bits(host_bits(y))
+        hm = host_f(hmax)
+        for p in range(N // 128):
+            assert np.array_equal(hm[:, p], hf[:, p * 128:(p + 1) * 128].max(1))
 
 
 @pytest.mark.parametrize("MNK", [(600, 1536, 512), (4200, 4600, 1024), (333, 1000, 8960)])
