@@ -23,6 +23,8 @@
 //   FVSR_EPI_GATE_ADD  C = bf16(res + bf16(gate[n] * y))
 // Workgroups are renumbered so each XCD (workgroup ids are dispatched round
 // robin over the 8 XCDs) walks a contiguous, M-grouped range of tiles.
+#include <utility>
+
 #include "common.h"
 
 // Buffer loads straight into LDS (buffer_load_dwordx4 ... lds): the 16 bytes
@@ -93,11 +95,12 @@ FVSR_DEV void zero_acc(v16f (&acc)[4][4]) {
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 }
 
-FVSR_DEV void mfma_block(v16f (&acc)[4][4], const v8i (&fa)[4], const v8i (&fb)[4]) {
+template <int MJ>
+FVSR_DEV void mfma_block(v16f (&acc)[4][MJ], const v8i (&fa)[MJ], const v8i (&fb)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < MJ; ++j)
       acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i], fa[j], acc[i][j], 0, 0,
                                                                    0, 0, 0, 0);
 }
@@ -215,36 +218,53 @@ FVSR_DEV void epilogue(const v16f (&acc)[4][4], const CTile& ct, int64_t m0, int
 // ---------------------------------------------------------------------------
 // Main loop, K % 64 == 0 and K >= 256: persistent direct-to-LDS ring.
 // ---------------------------------------------------------------------------
+// Tile shapes of the ring kernel: 256 output columns (B rows) by TM = 64 * MJ
+// output rows (A rows); each of the 4 waves owns TM / 2 rows (MJ blocks of
+// 32) by 128 columns (4 blocks).  MJ = 4 (256 x 256) everywhere except where
+// a single round of 128-row tiles covers the output that 256-row tiles would
+// leave mostly idle (C1: 4224 x 1536 is 102 tiles of 256 rows, 198 of 128).
+template <int MJ>
+struct Tile {
+  static constexpr int TM = 64 * MJ;
+  static constexpr int kPairBytes = (TM + BN) * 128;  // 64 KB (MJ 4) or 48 KB (MJ 2)
+  static constexpr int kLoadsA = TM / 32;              // A loads per wave per pair
+};
+
 // The ring holds K in pairs of 64-byte steps: a pair slot keeps 128 bytes of
-// every A row and B row (64 KB), so each load covers whole 128-byte lines.
+// every A row and B row, so each load covers whole 128-byte lines.
 // 16-byte chunk c of row r sits at chunk position c ^ (r & 7) ^ ((r >> 3) & 1):
 // any 8 consecutive rows read at one logical chunk hit 8 distinct 16-byte
 // bank groups, and any 16 consecutive rows 16 distinct (row parity, chunk)
 // pairs, so ds_read_b128 is conflict-free whether the LDS serves 8 or 16
 // lanes per cycle.
-constexpr int kPairBytes = (BM + BN) * 128;  // 64 KB
 FVSR_DEV int swz128(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
 
 // Per-lane byte offsets of the 16-byte pieces this lane streams for one pair:
-// load t (of 8) of each operand covers rows 64*wave + 8*t .. +7, lane l taking
-// row 8*t + l/8 (clamped to the matrix) and the chunk that lands at position
-// l % 8.  Offsets fit 32 bits (checked on the host), so each load is a
-// uniform base plus a per-lane 32-bit offset.
+// load t of an operand covers 8 of the wave's rows (A: TM / 4 rows per wave,
+// B: 64), lane l taking row 8*t + l/8 (clamped to the matrix) and the chunk
+// that lands at position l % 8.  Offsets fit 32 bits (checked on the host),
+// so each load is a uniform base plus a per-lane 32-bit offset.
+template <int MJ>
 struct DmaOffs {
-  uint32_t a[8], b[8];
+  uint32_t a[Tile<MJ>::kLoadsA], b[8];
 };
 
-FVSR_DEV void dma_offsets(DmaOffs& o, int64_t m0, int64_t n0, int64_t M, int64_t N, int64_t lda,
-                          int64_t ldb, int wave, int lane) {
+template <int MJ>
+FVSR_DEV void dma_offsets(DmaOffs<MJ>& o, int64_t m0, int64_t n0, int64_t M, int64_t N,
+                          int64_t lda, int64_t ldb, int wave, int lane) {
   const int rl = lane >> 3;
+  const int c = lane & 7;
+#pragma unroll
+  for (int t = 0; t < Tile<MJ>::kLoadsA; ++t) {
+    const int r = wave * (Tile<MJ>::TM / 4) + t * 8 + rl;
+    const int64_t ga = m0 + r < M ? m0 + r : M - 1;
+    o.a[t] = (uint32_t)(ga * lda + swz128(r, c) * 16);  // the swizzle is an involution in c
+  }
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     const int r = wave * 64 + t * 8 + rl;
-    const int c = swz128(r, lane & 7);  // the swizzle is an involution in c
-    const int64_t ga = m0 + r < M ? m0 + r : M - 1;
     const int64_t gb = n0 + r < N ? n0 + r : N - 1;
-    o.a[t] = (uint32_t)(ga * lda + c * 16);
-    o.b[t] = (uint32_t)(gb * ldb + c * 16);
+    o.b[t] = (uint32_t)(gb * ldb + swz128(r, c) * 16);
   }
 }
 
@@ -257,14 +277,17 @@ FVSR_DEV i32x4_t make_rsrc(const void* base, uint32_t bytes = 0xffffffffu) {
 
 // Stream one pair (A and B bytes [k0, k0+128) of the tile's rows) into a pair
 // slot.  The per-lane offsets stay in VGPRs and k0 rides in the scalar offset.
-FVSR_DEV void issue_pair(uint8_t LDS_AS* slot, i32x4_t ra, i32x4_t rb, int k0, const DmaOffs& o,
-                         int wave) {
+template <int MJ>
+FVSR_DEV void issue_pair(uint8_t LDS_AS* slot, i32x4_t ra, i32x4_t rb, int k0,
+                         const DmaOffs<MJ>& o, int wave) {
+  constexpr int LA = Tile<MJ>::kLoadsA;
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const int seg = wave * 8 + t;
-    fvsr_buffer_load_lds(ra, (void LDS_AS*)(slot + seg * 1024), 16, (int)o.a[t], k0, 0, 0);
-    fvsr_buffer_load_lds(rb, (void LDS_AS*)(slot + BM * 128 + seg * 1024), 16, (int)o.b[t], k0,
-                         0, 0);
+    if (t < LA)
+      fvsr_buffer_load_lds(ra, (void LDS_AS*)(slot + (wave * LA + t) * 1024), 16, (int)o.a[t],
+                           k0, 0, 0);
+    fvsr_buffer_load_lds(rb, (void LDS_AS*)(slot + Tile<MJ>::TM * 128 + (wave * 8 + t) * 1024),
+                         16, (int)o.b[t], k0, 0, 0);
   }
 }
 
@@ -277,15 +300,16 @@ FVSR_DEV v8i read_frag(const uint8_t LDS_AS* base, int r, int c0) {
              (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
-// All fragments of one step (A quadrant rows, then B quadrant rows).
+// All fragments of one step (the wave's A rows, then its B rows).
+template <int MJ>
 FVSR_DEV void read_step(const uint8_t LDS_AS* slot, int hs, int wm, int wn, int lane,
-                        v8i (&fa)[4], v8i (&fb)[4]) {
+                        v8i (&fa)[MJ], v8i (&fb)[4]) {
   const int c0 = 4 * hs + 2 * (lane >> 5);
-  const int ra = wm * 128 + (lane & 31), rb = wn * 128 + (lane & 31);
+  const int ra = wm * (32 * MJ) + (lane & 31), rb = wn * 128 + (lane & 31);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) fa[j] = read_frag(slot, ra + 32 * j, c0);
+  for (int j = 0; j < MJ; ++j) fa[j] = read_frag(slot, ra + 32 * j, c0);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fb[i] = read_frag(slot + BM * 128, rb + 32 * i, c0);
+  for (int i = 0; i < 4; ++i) fb[i] = read_frag(slot + Tile<MJ>::TM * 128, rb + 32 * i, c0);
 }
 
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
@@ -311,14 +335,31 @@ struct RingCtx {
 //     per-lane offsets `o`: the next tile's when past the end) -- two steps
 //     ahead of the reads that need it;
 //   read step s+1's fragments (pair slot `rd`, half RH) into na/nb;
-//   run the 16 MFMAs of step s (ZERO: start the accumulators from 0).
-// The sixteen loads go out one per MFMA (a burst of them stalls the wave's
-// instruction stream) and the reads with the first eight MFMAs, leaving the
-// second half of the step for them to land.
-template <bool PAIR, int RH, bool ZERO>
-FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_t LDS_AS* rd,
-                        uint8_t LDS_AS* ds, v16f (&acc)[4][4], const v8i (&fa)[4],
-                        const v8i (&fb)[4], v8i (&na)[4], v8i (&nb)[4]) {
+//   run the 4 * MJ MFMAs of step s (ZERO: start the accumulators from 0).
+// The loads are spread evenly over the MFMAs (a burst of them stalls the
+// wave's instruction stream) and the reads go with the first half of the
+// MFMAs, leaving the second half of the step for them to land.
+// Scheduling of one step: MFMA q is preceded by its share of the NL loads
+// (PAIR steps) and, in the first half of the step, followed by its share of
+// the ND fragment reads.
+template <bool PAIR, int NM, int NL, int ND, int Q>
+FVSR_DEV void sched_slot() {
+  if (PAIR) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, NL * (Q + 1) / NM - NL * Q / NM, 0);
+  __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+  if (2 * Q < NM)
+    __builtin_amdgcn_sched_group_barrier(kSgDsRead, ND * (Q + 1) / (NM / 2) - ND * Q / (NM / 2),
+                                         0);
+}
+
+template <bool PAIR, int NM, int NL, int ND, int... Q>
+FVSR_DEV void sched_step(std::integer_sequence<int, Q...>) {
+  (sched_slot<PAIR, NM, NL, ND, Q>(), ...);
+}
+
+template <int MJ, bool PAIR, int RH, bool ZERO>
+FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs<MJ>& o, int k0, const uint8_t LDS_AS* rd,
+                        uint8_t LDS_AS* ds, v16f (&acc)[4][MJ], const v8i (&fa)[MJ],
+                        const v8i (&fb)[4], v8i (&na)[MJ], v8i (&nb)[4]) {
   __builtin_amdgcn_sched_barrier(0);  // nothing (MFMAs included) moves across a step boundary
   if (PAIR) {
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
@@ -327,24 +368,20 @@ FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs& o, int k0, const uint8_
     __builtin_amdgcn_sched_barrier(0);
     issue_pair(ds, c.ra, c.rb, k0, o, c.wave);
   }
-  read_step(rd, RH, c.wm, c.wn, c.lane, na, nb);
+  read_step<MJ>(rd, RH, c.wm, c.wn, c.lane, na, nb);
   if (ZERO) {
     const v16f z = {};
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < MJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[i], fa[j], z, 0, 0, 0, 0,
                                                                      0, 0);
   } else {
-    mfma_block(acc, fa, fb);
+    mfma_block<MJ>(acc, fa, fb);
   }
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    if (PAIR) __builtin_amdgcn_sched_group_barrier(kSgVmemRead, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-    if (q < 8) __builtin_amdgcn_sched_group_barrier(kSgDsRead, 2, 0);
-  }
+  sched_step<PAIR, 4 * MJ, Tile<MJ>::kLoadsA + 8, 2 * (MJ + 4)>(
+      std::make_integer_sequence<int, 4 * MJ>{});
 }
 
 // Per-wave epilogue area: 32 rows x 64 columns of bf16 staging (4 KB, one
@@ -356,18 +393,20 @@ constexpr int kEpiStageBytes = 32 * 128;
 constexpr int kEpiWaveBytes = kEpiStageBytes + 3 * 128 * 4;
 FVSR_DEV int epi_off(int row, int unit) { return row * 128 + ((unit ^ (row & 15)) << 3); }
 
-// This lane's share of the quadrant's parameters (rows / columns q*64 + lane),
-// loaded into registers ahead of time and parked in LDS by put_epi_params.
+// This lane's share of the wave's parameters (rows / columns q*64 + lane of
+// the wave's `wrows` rows and 128 columns; rows past them are loaded but not
+// used), loaded into registers ahead of time and parked in LDS by
+// put_epi_params.
 struct EpiParamRegs {
   float sa[2], sb[2];
   uint32_t bias[2];
 };
 
 FVSR_DEV void fetch_epi_params(EpiParamRegs& r, const EpiArgs& e, int64_t m0, int64_t n0,
-                               int64_t M, int64_t N, int wm, int wn, int lane) {
+                               int64_t M, int64_t N, int wm, int wn, int wrows, int lane) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int64_t m = m0 + wm * 128 + q * 64 + lane, n = n0 + wn * 128 + q * 64 + lane;
+    const int64_t m = m0 + wm * wrows + q * 64 + lane, n = n0 + wn * 128 + q * 64 + lane;
     const int64_t mc = m < M ? m : M - 1, nc = n < N ? n : N - 1;
     r.sa[q] = e.sa[e.sa_row ? mc : 0];
     r.sb[q] = e.sb[e.sb_col ? nc : 0];
@@ -511,7 +550,8 @@ FVSR_DEV void fast_params(FastParams& fp, const uint8_t LDS_AS* prm, int ip, int
 }
 
 // Convert pass (ip, j) and write it to the staging area.
-FVSR_DEV void fast_stage(const v16f (&acc)[4][4], const FastParams& fp, float sam,
+template <int MJ>
+FVSR_DEV void fast_stage(const v16f (&acc)[4][MJ], const FastParams& fp, float sam,
                          uint16_t LDS_AS* stg, int ip, int j, int row, int h) {
 #pragma unroll
   for (int ii = 0; ii < 2; ++ii)
@@ -552,40 +592,42 @@ FVSR_DEV void fast_store(const u32x4_t (&v)[4], float (&vmax)[4], i32x4_t rc, in
   }
 }
 
-template <int EPI>
-FVSR_DEV void epi_fast(const v16f (&acc)[4][4], uint16_t LDS_AS* stg, const uint8_t LDS_AS* prm,
+template <int EPI, int MJ>
+FVSR_DEV void epi_fast(const v16f (&acc)[4][MJ], uint16_t LDS_AS* stg, const uint8_t LDS_AS* prm,
                        int64_t mw, int64_t nw, int64_t M, const EpiArgs& e, i32x4_t rc,
                        int lane) {
   const float LDS_AS* sa_l = (const float LDS_AS*)prm;
   const int h = lane >> 5, row = lane & 31;
-  float sam[4];
+  float sam[MJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sam[j] = sa_l[j * 32 + row];
+  for (int j = 0; j < MJ; ++j) sam[j] = sa_l[j * 32 + row];
   // Store offset of row lane / 8, chunk lane % 8; each pass adds its row
   // block, row group and column half (all in the offset the range check
   // covers).
   const int voff = (int)(((mw + (lane >> 3)) * e.ldc + nw + (lane & 7) * 8) * 2);
-  float vmax[4][4];
+  float vmax[MJ][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < MJ; ++j)
 #pragma unroll
     for (int s = 0; s < 4; ++s) vmax[j][s] = -__builtin_huge_valf();
   FastParams fp;
   fast_params(fp, prm, 0, h);
-  fast_stage(acc, fp, sam[0], stg, 0, 0, row, h);
+  fast_stage<MJ>(acc, fp, sam[0], stg, 0, 0, row, h);
+  // Passes p = ip * MJ + j.
 #pragma unroll
-  for (int p = 0; p < 8; ++p) {
-    const int ip = p >> 2, j = p & 3;
+  for (int p = 0; p < 2 * MJ; ++p) {
+    const int ip = p / MJ, j = p % MJ;
     u32x4_t v[4];
     fast_read(stg, v, lane);
-    if (p == 3) fast_params(fp, prm, 1, h);
-    if (p < 7) fast_stage(acc, fp, sam[(p + 1) & 3], stg, (p + 1) >> 2, (p + 1) & 3, row, h);
+    if (p == MJ - 1) fast_params(fp, prm, 1, h);
+    if (p + 1 < 2 * MJ)
+      fast_stage<MJ>(acc, fp, sam[(p + 1) % MJ], stg, (p + 1) / MJ, (p + 1) % MJ, row, h);
     fast_store<EPI>(v, vmax[j], rc, voff, e.ldc, ip, j);
   }
   if (EPI == FVSR_EPI_ROWMAX) {
     // 8 lanes per row cover 64 columns per pass; both halves = the slab.
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < MJ; ++j)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         float v = vmax[j][s];
@@ -597,10 +639,11 @@ FVSR_DEV void epi_fast(const v16f (&acc)[4][4], uint16_t LDS_AS* stg, const uint
   }
 }
 
-FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t& n0) {
+FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int tile_rows, int64_t& m0,
+                          int64_t& n0) {
   int tm, tn;
   map_tile(t, tiles_m, tiles_n, tm, tn);
-  m0 = (int64_t)tm * BM;
+  m0 = (int64_t)tm * tile_rows;
   n0 = (int64_t)tn * BN;
 }
 
@@ -615,17 +658,19 @@ FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int64_t& m0, int64_t&
 // wave).  After a workgroup's last tile the same stream re-fetches that
 // tile's first pairs (harmless) and the workgroup drains its loads before it
 // exits.
-template <int EPI, bool DIRECT>
+template <int EPI, bool DIRECT, int MJ>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
                    int64_t ldb, int64_t M, int64_t N, int64_t K, EpiArgs ep) {
-  __shared__ __attribute__((aligned(1024))) uint8_t pair0[kPairBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t pair1[kPairBytes];
+  static_assert(MJ == 4 || (MJ == 2 && DIRECT), "128-row tiles take the fast epilogue only");
+  constexpr int TM = Tile<MJ>::TM;
+  __shared__ __attribute__((aligned(1024))) uint8_t pair0[Tile<MJ>::kPairBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t pair1[Tile<MJ>::kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t spare[4 * kEpiWaveBytes];
   uint8_t LDS_AS* p0 = (uint8_t LDS_AS*)pair0;
   uint8_t LDS_AS* p1 = (uint8_t LDS_AS*)pair1;
 
-  const int tiles_m = (int)((M + BM - 1) / BM), tiles_n = (int)((N + BN - 1) / BN);
+  const int tiles_m = (int)((M + TM - 1) / TM), tiles_n = (int)((N + BN - 1) / BN);
   const int tiles = tiles_m * tiles_n;
   int t = blockIdx.x;
   if (t >= tiles) return;
@@ -639,53 +684,55 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
 
   RingCtx c{make_rsrc(A), make_rsrc(B), wave, wm, wn, lane};
   int64_t m0, n0;
-  tile_origin(t, tiles_m, tiles_n, m0, n0);
-  DmaOffs cur;
-  dma_offsets(cur, m0, n0, M, N, lda, ldb, wave, lane);
-  issue_pair(p0, c.ra, c.rb, 0, cur, wave);
-  issue_pair(p1, c.ra, c.rb, 128, cur, wave);
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(16, 15));
+  tile_origin(t, tiles_m, tiles_n, TM, m0, n0);
+  DmaOffs<MJ> cur;
+  dma_offsets<MJ>(cur, m0, n0, M, N, lda, ldb, wave, lane);
+  issue_pair<MJ>(p0, c.ra, c.rb, 0, cur, wave);
+  issue_pair<MJ>(p1, c.ra, c.rb, 128, cur, wave);
+  // The first pair (the older half of the loads in flight) has landed.
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(Tile<MJ>::kLoadsA + 8, 15));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-  v16f acc[4][4];
-  v8i fa[4], fb[4], na[4], nb[4];
-  read_step(p0, 0, wm, wn, lane, fa, fb);
+  v16f acc[4][MJ];
+  v8i fa[MJ], fb[4], na[MJ], nb[4];
+  read_step<MJ>(p0, 0, wm, wn, lane, fa, fb);
 
   for (;;) {
     // First trip: steps 0-3 (accumulators start from 0 at step 0).
-    ring_step<false, 1, true>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
-    ring_step<true, 0, false>(c, cur, 2 * 128, p1, p0, acc, na, nb, fa, fb);
-    ring_step<false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
-    ring_step<true, 0, false>(c, cur, 3 * 128, p0, p1, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, true>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false>(c, cur, 2 * 128, p1, p0, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false>(c, cur, 3 * 128, p0, p1, acc, na, nb, fa, fb);
     // Steady state: steps kt .. kt+3 load pairs kt/2 + 2 and kt/2 + 3.
     for (int kt = 4; kt < KT - 4; kt += 4) {
-      ring_step<false, 1, false>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
-      ring_step<true, 0, false>(c, cur, (kt + 4) * 64, p1, p0, acc, na, nb, fa, fb);
-      ring_step<false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
-      ring_step<true, 0, false>(c, cur, (kt + 6) * 64, p0, p1, acc, na, nb, fa, fb);
+      ring_step<MJ, false, 1, false>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+      ring_step<MJ, true, 0, false>(c, cur, (kt + 4) * 64, p1, p0, acc, na, nb, fa, fb);
+      ring_step<MJ, false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+      ring_step<MJ, true, 0, false>(c, cur, (kt + 6) * 64, p0, p1, acc, na, nb, fa, fb);
     }
     // Last trip: steps KT-4 .. KT-1; their loads are the next tile's pairs 0
     // and 1 and the last reads are the next tile's step 0.
     const int tn = t + (int)gridDim.x;
     int64_t m1 = m0, n1 = n0;
-    if (tn < tiles) tile_origin(tn, tiles_m, tiles_n, m1, n1);
-    DmaOffs nxt;
-    dma_offsets(nxt, m1, n1, M, N, lda, ldb, wave, lane);
+    if (tn < tiles) tile_origin(tn, tiles_m, tiles_n, TM, m1, n1);
+    DmaOffs<MJ> nxt;
+    dma_offsets<MJ>(nxt, m1, n1, M, N, lda, ldb, wave, lane);
     // This tile's epilogue parameters load under the last trip's MFMAs.
     EpiParamRegs epr;
-    fetch_epi_params(epr, ep, m0, n0, M, N, wm, wn, lane);
-    ring_step<false, 1, false>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
-    ring_step<true, 0, false>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
-    ring_step<false, 1, false>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
-    ring_step<true, 0, false>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
+    fetch_epi_params(epr, ep, m0, n0, M, N, wm, wn, TM / 2, lane);
+    ring_step<MJ, false, 1, false>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, false>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
 
-    // Epilogue (fa/fb now hold the next tile's step-0 fragments): eight
-    // passes of 32 rows x 64 columns through the wave's own staging area.
+    // Epilogue (fa/fb now hold the next tile's step-0 fragments): passes of
+    // 32 rows x 64 columns through the wave's own staging area.
     const int el = lane_here();
-    const int64_t mw = m0 + wm * 128, nw = n0 + wn * 128;
+    const int64_t mw = m0 + wm * (TM / 2), nw = n0 + wn * 128;
     put_epi_params(epr, prm, el);
-    if (DIRECT) {
-      epi_fast<EPI>(acc, stg, prm, mw, nw, M, ep, make_rsrc(ep.c, (uint32_t)(M * ep.ldc * 2)), el);
+    if constexpr (DIRECT) {
+      epi_fast<EPI, MJ>(acc, stg, prm, mw, nw, M, ep,
+                        make_rsrc(ep.c, (uint32_t)(M * ep.ldc * 2)), el);
     } else {
       float vmax[4][4];
 #pragma unroll
@@ -812,17 +859,26 @@ void gemm_fp8_generic(const uint8_t* __restrict__ A, int64_t lda, const uint8_t*
   epilogue<EPI>(acc, ct, m0, n0, M, N, ep, wm, wn, lane);
 }
 
+enum class Path { kGeneric, kRing, kRingFast, kRingFast128 };
+
 template <int EPI>
-void launch(bool ring, unsigned grid, hipStream_t st, const uint8_t* a, int64_t lda,
+void launch(Path path, unsigned grid, hipStream_t st, const uint8_t* a, int64_t lda,
             const uint8_t* b, int64_t ldb, int64_t M, int64_t N, int64_t K, const EpiArgs& ep) {
-  // The fast epilogue needs whole column tiles; gate-add keeps the general
-  // one, which loads its residual rows ahead of the stores.
-  if (ring && EPI != FVSR_EPI_GATE_ADD && ep.direct && N % BN == 0)
-    hipLaunchKernelGGL((gemm_fp8_ring<EPI, EPI != FVSR_EPI_GATE_ADD>), dim3(grid), dim3(kThreads),
-                       0, st, a, lda, b, ldb, M, N, K, ep);
-  else if (ring)
-    hipLaunchKernelGGL((gemm_fp8_ring<EPI, false>), dim3(grid), dim3(kThreads), 0, st, a, lda, b,
-                       ldb, M, N, K, ep);
+  if constexpr (EPI != FVSR_EPI_GATE_ADD) {  // gate-add keeps the general epilogue
+    if (path == Path::kRingFast) {
+      hipLaunchKernelGGL((gemm_fp8_ring<EPI, true, 4>), dim3(grid), dim3(kThreads), 0, st, a, lda,
+                         b, ldb, M, N, K, ep);
+      return;
+    }
+    if (path == Path::kRingFast128) {
+      hipLaunchKernelGGL((gemm_fp8_ring<EPI, true, 2>), dim3(grid), dim3(kThreads), 0, st, a, lda,
+                         b, ldb, M, N, K, ep);
+      return;
+    }
+  }
+  if (path != Path::kGeneric)
+    hipLaunchKernelGGL((gemm_fp8_ring<EPI, false, 4>), dim3(grid), dim3(kThreads), 0, st, a, lda,
+                       b, ldb, M, N, K, ep);
   else
     hipLaunchKernelGGL(gemm_fp8_generic<EPI>, dim3(grid), dim3(kThreads), 0, st, a, lda, b, ldb,
                        M, N, K, ep);
@@ -830,14 +886,13 @@ void launch(bool ring, unsigned grid, hipStream_t st, const uint8_t* a, int64_t 
 
 // Workgroups of the persistent kernel: one per CU, rounded down to a multiple
 // of the 8 XCDs.
-unsigned persistent_grid(int64_t tiles) {
+int64_t persistent_slots() {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       cus < 8)
     cus = 256;
-  const int64_t g = (cus / 8) * 8;
-  return (unsigned)(tiles < g ? tiles : g);
+  return (cus / 8) * 8;
 }
 
 }  // namespace
@@ -873,17 +928,27 @@ extern "C" int fvsr_fp8_gemm(const void* a, int64_t lda, const float* sa, int sa
   // offset of either operand within 32 bits.
   const bool ring = K % 256 == 0 && K >= 512 && K < 0x7fffffffLL && (M - 1) * lda + K <= 0xffffffffLL &&
                     (N - 1) * ldb + K <= 0xffffffffLL;
-  const unsigned grid = ring ? persistent_grid(tiles) : (unsigned)tiles;
+  // The fast epilogue needs whole column tiles.  128-row tiles when one
+  // round of them covers the output (a 128-row tile takes about half as long
+  // as a 256-row one, and 256-row tiles would then be a partial round too).
+  const bool fast = ring && epilogue != FVSR_EPI_GATE_ADD && direct && N % BN == 0;
+  const int64_t slots = persistent_slots();
+  const int64_t tiles128 = ((M + 127) / 128) * ((N + BN - 1) / BN);
+  const Path path = !ring ? Path::kGeneric
+                    : !fast ? Path::kRing
+                    : tiles128 <= slots ? Path::kRingFast128 : Path::kRingFast;
+  const int64_t units = path == Path::kRingFast128 ? tiles128 : tiles;
+  const unsigned grid = (unsigned)(ring && units > slots ? slots : units);
   const uint8_t *ap = (const uint8_t*)a, *bp = (const uint8_t*)b;
   switch (epilogue) {
     case FVSR_EPI_BIAS:
-      launch<FVSR_EPI_BIAS>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_BIAS>(path, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
     case FVSR_EPI_ROWMAX:
-      launch<FVSR_EPI_ROWMAX>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_ROWMAX>(path, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
     default:
-      launch<FVSR_EPI_GATE_ADD>(ring, grid, st, ap, lda, bp, ldb, M, N, K, ep);
+      launch<FVSR_EPI_GATE_ADD>(path, grid, st, ap, lda, bp, ldb, M, N, K, ep);
       break;
   }
   return fvsr_launch_status();

@@ -329,11 +329,14 @@ def test_fp8_gemm_ring_shapes(ops, MNK):
 
 
 @pytest.mark.parametrize("epi", ["bias", "rowmax"])
-@pytest.mark.parametrize("MNK", [(4224, 1536, 1536), (77, 512, 512), (1000, 2560, 768)])
+@pytest.mark.parametrize("MNK", [(4224, 1536, 1536), (77, 512, 512), (1000, 2560, 768),
+                                 (2100, 8960, 512)])
 def test_fp8_gemm_direct_epilogue_rows_past_m(ops, MNK, epi):
-    """Whole column tiles store straight from the accumulators, with rows past
-    M dropped by the store descriptor's byte range: the output is a view of the
-    first M rows of a larger buffer whose remaining rows must keep a sentinel."""
+    """Whole column tiles take the fast epilogue, whose stores of rows past M
+    are dropped by the store descriptor's byte range: the output is a view of
+    the first M rows of a larger buffer whose remaining rows must keep a
+    sentinel.  The first three shapes fit one round of 128-row tiles (the
+    128-row kernel), the last one does not (256-row tiles)."""
     from flashvsr_sm89_ops import _lib
     M, N, K = MNK
     a, b, sa, sb, bias = _gemm_inputs(M, N, K, seed=11 * M + N)
