@@ -48,84 +48,162 @@ FVSR_DEV int k_swz(int r, int c) { return c ^ (r & 15); }
 // half-wave read adjacent 32-byte column blocks; this spreads them over 64 banks.
 FVSR_DEV int v_swz(int r, int c) { return c ^ ((r & 3) << 2); }
 
-// Stream one 64-key half of key block `blk` into `stage`.  Each wave issues
-// 8 direct loads of 1 KB (4 rows); lane i of a load lands at row 4*seg + i/16,
-// physical chunk i%16, and fetches the logical chunk that belongs there.
-// The token indices are gathered first (one wait), then the eight loads go
-// out back to back.  Waves 0-1 stream K, waves 2-3 stream V.
+// Per-lane state of the K/V stream.  Each wave issues 8 direct loads of 1 KB
+// (4 rows of 256 bytes) per 64-key half: load t covers rows 4*seg .. 4*seg+3
+// of the tile, seg = (wave & 1) * 8 + t, lane i landing at row 4*seg + i/16,
+// physical chunk i%16 and fetching the logical chunk that belongs there.
+// Waves 0-1 stream K, waves 2-3 stream V.  The chunk a lane fetches depends
+// only on t % 4 (K) or not at all (V), so `lbase[t % 4]` (the tile base
+// pointer plus the chunk offset) is fixed for the whole kernel, and a load's
+// address is lbase + token row * row stride: one multiply-add per load.
+// With a token map the 8 rows' tokens of the next-but-one half are gathered
+// one step ahead, so no load ever waits on the map.
+struct Stream {
+  const uint8_t* lbase[4];
+  uint32_t ts2;             // token row stride in bytes
+  const int32_t* kv_map;
+  int blk[2];               // key blocks of the current and the next block step
+  int tok[8];               // MAP: tokens of the rows of the next half to issue
+};
+
+FVSR_DEV int stream_row(int wave, int t, int lane) { return ((wave & 1) * 8 + t) * 4 + (lane >> 4); }
+
+// First position of half `hf` of key block `blk`.
+FVSR_DEV int64_t half_pos(int blk, int hf) { return (int64_t)blk * kBlk + hf * kHalf; }
+
 template <bool MAP>
-FVSR_DEV void issue_half(uint8_t LDS_AS* stage, const uint16_t* __restrict__ kh,
-                         const uint16_t* __restrict__ vh, int64_t ts,
-                         const int32_t* __restrict__ kv_map, int blk, int half, int wave,
-                         int lane) {
-  const bool isv = wave >= 2;  // wave-uniform
-  const uint16_t* base = isv ? vh : kh;
-  uint8_t LDS_AS* tile = stage + (isv ? kTile : 0);
-  int64_t tok[8];
+FVSR_DEV void gather_tokens(Stream& s, int blk, int hf, int wave, int lane) {
+  if (MAP) {
+    const int64_t p0 = half_pos(blk, hf);
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const int r = ((wave & 1) * 8 + t) * 4 + (lane >> 4);
-    const int64_t pos = (int64_t)blk * kBlk + half * kHalf + r;
-    tok[t] = MAP ? (int64_t)kv_map[pos] : pos;
+    for (int t = 0; t < 8; ++t) s.tok[t] = s.kv_map[p0 + stream_row(wave, t, lane)];
   }
+}
+
+// Token rows are non-negative and below 2^31, so a load's address is one
+// 32 x 32 -> 64-bit multiply-add onto the lane's base pointer.
+template <bool MAP>
+FVSR_DEV void issue_half(uint8_t LDS_AS* stage, const Stream& s, int blk, int hf, int wave,
+                         int lane) {
+  uint8_t LDS_AS* tile = stage + (wave >= 2 ? kTile : 0);
+  const uint32_t p0 = MAP ? 0u : (uint32_t)half_pos(blk, hf);
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
-    const int seg = (wave & 1) * 8 + t;  // 1 KB segment = rows 4*seg .. 4*seg+3
-    const int r = seg * 4 + (lane >> 4);
-    const int p = lane & 15;
-    const int c = isv ? v_swz(r, p) : k_swz(r, p);  // the swizzles are involutions
-    __builtin_amdgcn_global_load_lds(base + tok[t] * ts + c * 8,
+    const int seg = (wave & 1) * 8 + t;
+    const uint32_t row = MAP ? (uint32_t)s.tok[t] : p0 + (uint32_t)stream_row(wave, t, lane);
+    __builtin_amdgcn_global_load_lds(s.lbase[t & 3] + (uint64_t)row * s.ts2,
                                      (void LDS_AS*)(tile + seg * 1024), 16, 0, 0);
   }
 }
 
 struct StepCtx {
-  const uint16_t* kh;
-  const uint16_t* vh;
-  int64_t ts;
-  const int32_t* kv_map;
-  const int32_t* blocks;
   int steps, wave, lane, half, g16, s16;
   float scale_log2;
 };
 
+// The four V^T operands of dim subtile jd (steps (jk, gp) -> j = jk*2 + gp),
+// read with inline-asm ds_read_b64_tr_b16: the compiler cannot tell the
+// builtin's reads from the direct loads streaming into the other stage and
+// would wait for those loads (vmcnt(0)) first.  The caller waits (lgkmcnt)
+// before using the operands.
+FVSR_DEV void read_vt(const uint8_t LDS_AS* vt, const StepCtx& c, int jd, u32x4_t (&vf)[4]) {
+  const int dcol = jd * 32 + (c.g16 & 1) * 16 + 4 * (c.s16 & 3);
+  const int cch = dcol >> 3, cof = (dcol & 7) * 2;
+  const int rl = c.half * 4 + (c.s16 >> 2);  // row within each 16-key group; rl & 3 = (s16 >> 2) & 3
+  const uint32_t a = (uint32_t)(uintptr_t)vt + rl * 256 + (v_swz(rl, cch) << 4) + cof;
+#define FVSR_TR(J, OFF, DST)                                                            \
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(DST) : "v"(a), "i"(OFF))
+  u32x2_t lo0, hi0, lo1, hi1, lo2, hi2, lo3, hi3;
+  FVSR_TR(0, 0 * 256, lo0);
+  FVSR_TR(0, 8 * 256, hi0);
+  FVSR_TR(1, 16 * 256, lo1);
+  FVSR_TR(1, 24 * 256, hi1);
+  FVSR_TR(2, 32 * 256, lo2);
+  FVSR_TR(2, 40 * 256, hi2);
+  FVSR_TR(3, 48 * 256, lo3);
+  FVSR_TR(3, 56 * 256, hi3);
+#undef FVSR_TR
+  vf[0] = u32x4_t{lo0[0], lo0[1], hi0[0], hi0[1]};
+  vf[1] = u32x4_t{lo1[0], lo1[1], hi1[0], hi1[1]};
+  vf[2] = u32x4_t{lo2[0], lo2[1], hi2[0], hi2[1]};
+  vf[3] = u32x4_t{lo3[0], lo3[1], hi3[0], hi3[1]};
+}
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14 (63 =
+// left open), expcnt 6:4 (left open), lgkmcnt 11:8.
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4) | (0 << 8);
+
+FVSR_DEV void wait_lds() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
 // One 64-key half step: wait for `cur`, start streaming step it+1 into
-// `nxt`, then S^T, softmax and O^T on `cur`.  `cur` and `nxt` are distinct
-// LDS objects, so the compiler can tell the direct loads into `nxt` apart from
-// the reads of `cur` and does not serialise them.
+// `nxt` (and gather the tokens of step it+2), then S^T, softmax and O^T on
+// `cur`.  All sixteen K fragments are read before the S^T MFMAs and all
+// sixteen V^T fragments before the softmax, so the MFMAs never wait on a
+// read issued just before them and the V reads complete under the softmax.
+// `cur` and `nxt` are distinct LDS objects, so the compiler can tell the
+// direct loads into `nxt` apart from the reads of `cur` and does not
+// serialise them.
 template <bool MAP>
 FVSR_DEV void bsa_step(uint8_t LDS_AS* cur, uint8_t LDS_AS* nxt, int it, const StepCtx& c,
-                       const u32x4_t (&qf)[8], v16f (&acc)[4], float& m_run, float& l_run) {
+                       Stream& st, const u32x4_t (&qf)[8], v16f (&acc)[4], float& m_run,
+                       float& l_run) {
   __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of step `it` have landed
   __syncthreads();                // ... and everyone's; `nxt` is no longer being read
-  if (it + 1 < c.steps)
-    issue_half<MAP>(nxt, c.kh, c.vh, c.ts, c.kv_map, c.blocks[(it + 1) >> 1], (it + 1) & 1,
-                    c.wave, c.lane);
+  // Step it+1 is the second half of this block (it even) or the first half of
+  // the next; step it+2 the first or second half of the next block.
+  const int hf = it & 1;
+  if (it + 1 < c.steps) issue_half<MAP>(nxt, st, st.blk[hf], hf ^ 1, c.wave, c.lane);
+  if (MAP && it + 2 < c.steps) gather_tokens<MAP>(st, st.blk[1], hf, c.wave, c.lane);
   const uint8_t LDS_AS* kt = cur;
   const uint8_t LDS_AS* vt = cur + kTile;
   const int lane = c.lane, half = c.half;
 
   // S^T[key][q] for the two 32-key subtiles of this half.
+  u32x4_t kf[2][8];
+#pragma unroll
+  for (int jk = 0; jk < 2; ++jk) {
+    const int r = jk * 32 + (lane & 31);
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+      kf[jk][kk] = *(const u32x4_t LDS_AS*)(kt + r * 256 + (k_swz(r, kk * 2 + half) << 4));
+  }
   v16f s[2];
 #pragma unroll
   for (int jk = 0; jk < 2; ++jk) {
+    const v16f z = {};
+    s[jk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(kf[jk][0]), as_bf(qf[0]), z, 0, 0, 0);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) s[jk][e] = 0.0f;
-    const int r = jk * 32 + (lane & 31);
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      const u32x4_t kf = *(const u32x4_t LDS_AS*)(kt + r * 256 + (k_swz(r, kk * 2 + half) << 4));
-      s[jk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(kf), as_bf(qf[kk]), s[jk], 0, 0, 0);
-    }
+    for (int kk = 1; kk < 8; ++kk)
+      s[jk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(kf[jk][kk]), as_bf(qf[kk]), s[jk], 0,
+                                                      0, 0);
   }
+  __builtin_amdgcn_sched_group_barrier(0x100, 16, 0);  // the 16 K reads
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);  // then the 16 S^T MFMAs
 
+  // V^T operands of step (jd, jk, gp): lane half h supplies keys kb0 + 0..3
+  // and kb0 + 8 + 0..3, kb0 = jk*32 + gp*16 + h*4; a transposed read gives
+  // lane (g16, s16) dims dbase + s16 of keys kb..kb+3 from the 8 bytes at row
+  // kb + s16/4, dims dbase + 4*(s16%4).  Dim subtiles 0-1 are read before the
+  // softmax, 2-3 under the MFMAs of 0-1.
+  u32x4_t vf[4][4];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int jd = 0; jd < 2; ++jd) read_vt(vt, c, jd, vf[jd]);
   // Online softmax for this lane's query over the 64 keys of the half.
   float mx = -__builtin_huge_valf();
 #pragma unroll
   for (int jk = 0; jk < 2; ++jk)
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[jk][e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * c.scale_log2;
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false,
+                                                     false);  // lane l and l ^ 32
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c.scale_log2;
+  }
   if (__ballot(mx > m_run + 8.0f) != 0) {  // move the max (wave-uniform)
     asm volatile("" :::);  // keep this a branch: the rescale is rare after the first steps
     const float m_new = fmaxf(m_run, mx);
@@ -156,30 +234,17 @@ FVSR_DEV void bsa_step(uint8_t LDS_AS* cur, uint8_t LDS_AS* nxt, int it, const S
   }
   l_run += psum;
 
-  // O^T[d][q] += V^T[d][key] P^T[key][q].  Step (jk, gp): lane half h
-  // supplies keys kb0 + 0..3 and kb0 + 8 + 0..3, kb0 = jk*32 + gp*16 + h*4;
-  // a transposed read gives lane (g16, s16) dims dbase + s16 of keys kb..kb+3
-  // from the 8 bytes at row kb + s16/4, dims dbase + 4*(s16%4).
+  // O^T[d][q] += V^T[d][key] P^T[key][q].
+  wait_lds();  // V operands of dim subtiles 0-1
+  read_vt(vt, c, 2, vf[2]);
+  read_vt(vt, c, 3, vf[3]);
 #pragma unroll
   for (int jd = 0; jd < 4; ++jd) {
-    const int dcol = jd * 32 + (c.g16 & 1) * 16 + 4 * (c.s16 & 3);
-    const int cch = dcol >> 3, cof = (dcol & 7) * 2;
+    if (jd == 2) wait_lds();  // ... and 2-3
 #pragma unroll
-    for (int jk = 0; jk < 2; ++jk) {
-#pragma unroll
-      for (int gp = 0; gp < 2; ++gp) {
-        const int r0 = jk * 32 + gp * 16 + half * 4 + (c.s16 >> 2);
-        const int r1 = r0 + 8;
-        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (v4s LDS_AS*)(vt + r0 * 256 + (v_swz(r0, cch) << 4) + cof));
-        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (v4s LDS_AS*)(vt + r1 * 256 + (v_swz(r1, cch) << 4) + cof));
-        const u32x2_t l2 = __builtin_bit_cast(u32x2_t, lo), h2 = __builtin_bit_cast(u32x2_t, hi);
-        const u32x4_t vf = {l2[0], l2[1], h2[0], h2[1]};
-        acc[jd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(vf), as_bf(pf[jk * 2 + gp]),
-                                                          acc[jd], 0, 0, 0);
-      }
-    }
+    for (int j = 0; j < 4; ++j)
+      acc[jd] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf(vf[jd][j]), as_bf(pf[j]), acc[jd], 0,
+                                                        0, 0);
   }
 }
 
@@ -205,11 +270,26 @@ void bsa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   const int lane = threadIdx.x & 63, half = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = cnt[(int64_t)h * NQ + qb];
-  StepCtx c{k + (int64_t)h * kv_hs, v + (int64_t)h * kv_hs, kv_ts, kv_map,
-            sel + ((int64_t)h * NQ + qb) * maxk, 2 * n, wave, lane, half, lane >> 4, lane & 15,
-            scale_log2};
-
-  if (c.steps > 0) issue_half<MAP>(st0, c.kh, c.vh, c.ts, c.kv_map, c.blocks[0], 0, wave, lane);
+  const StepCtx c{2 * n, wave, lane, half, lane >> 4, lane & 15, scale_log2};
+  const int32_t* blocks = sel + ((int64_t)h * NQ + qb) * maxk;
+  Stream st;
+  {
+    const uint16_t* base = (wave >= 2 ? v : k) + (int64_t)h * kv_hs;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int r = stream_row(wave, t, lane), p = lane & 15;
+      st.lbase[t] = (const uint8_t*)(base + (wave >= 2 ? v_swz(r, p) : k_swz(r, p)) * 8);  // involutions
+    }
+    st.ts2 = (uint32_t)(kv_ts * 2);
+    st.kv_map = kv_map;
+  }
+  if (n > 0) {
+    st.blk[0] = blocks[0];
+    st.blk[1] = blocks[n > 1 ? 1 : 0];
+    gather_tokens<MAP>(st, st.blk[0], 0, wave, lane);
+    issue_half<MAP>(st0, st, st.blk[0], 0, wave, lane);
+    gather_tokens<MAP>(st, st.blk[0], 1, wave, lane);
+  }
 
   // This lane's query (MFMA column) and its Q^T operand: d-step kk covers
   // dims kk*16 + half*8 .. +8.
@@ -229,12 +309,19 @@ void bsa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__
     for (int e = 0; e < 16; ++e) acc[jd][e] = 0.0f;
   float m_run = -__builtin_huge_valf(), l_run = 0.0f;
 
-  for (int it = 0; it < c.steps; it += 2) {  // steps is even: two halves per block
-    bsa_step<MAP>(st0, st1, it, c, qf, acc, m_run, l_run);
-    bsa_step<MAP>(st1, st0, it + 1, c, qf, acc, m_run, l_run);
+  for (int b = 0; b < n; ++b) {  // two 64-key halves per kept block
+    // The block after next loads under this block's steps (a full wait opens
+    // every step) and becomes st.blk[1] when the block moves on.
+    const int ahead = blocks[b + 2 < n ? b + 2 : n - 1];
+    bsa_step<MAP>(st0, st1, 2 * b, c, st, qf, acc, m_run, l_run);
+    bsa_step<MAP>(st1, st0, 2 * b + 1, c, st, qf, acc, m_run, l_run);
+    st.blk[0] = st.blk[1];
+    st.blk[1] = ahead;
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const auto lsw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run),
+                                                    false, false);
+  const float l_tot = __uint_as_float(lsw[0]) + __uint_as_float(lsw[1]);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   uint16_t* orow = o + qtok * o_ts + (int64_t)h * o_hs;
 #pragma unroll
