@@ -175,6 +175,19 @@ FVSR_DEV float quot_abs(float v, float r, float sc) {
   return fmaf(e, r, q0);
 }
 
+// The same quotient on the signed value, for code paths that hold unpacked
+// floats (no sign bits to gather): q0 = v * r, t = q0 * s - v (the negated
+// residual) and q0 - t * r.  Every step is odd in v under round-to-nearest, so
+// the result is -quot(|v|) for negative v, and equals quot_abs's value for
+// v > 0 (t is exactly -e, or both are +0).  For v = -0 it is -0 (q0 = -0,
+// t = +0, -0 - 0 = -0), so the conversion's own sign gives the code.  Checked
+// over the same pairs, both signs, by tests/native/fma_quotient_check.c.
+FVSR_DEV float quot_signed(float v, float r, float sc) {
+  const float q0 = v * r;
+  const float t = fmaf(q0, sc, -v);
+  return fmaf(t, -r, q0);
+}
+
 // Codes of one chunk (8 packed bf16 values) divided by s (r = fl(1/s),
 // sc = min(s, FLT_MAX)), every value bounded by the amax s was made from.
 // The sign bits of the inputs (bit 7 of bytes 1 and 3 of each dword) are

@@ -60,3 +60,30 @@ def test_fma_quotient_check_catches_a_dropped_correction():
                        check=True)
         r = subprocess.run([exe, "64", "3"], capture_output=True, text=True)
         assert r.returncode == 1 and " mismatches 0" not in r.stdout, r.stdout
+
+
+@pytest.mark.parametrize("plant", [
+    # no correction step in the signed form
+    ("const uint8_t got_signed = code_of(fmaf(t, -r, p0));",
+     "const uint8_t got_signed = code_of(p0); (void)t;"),
+    # the residual of quot_abs carried over to signed values: -0 then loses
+    # its sign (q0 = -0, e = +0, -0 + 0 = +0)
+    ("const float t = fmaf(p0, sc, -v);\n        const uint8_t got_signed = code_of(fmaf(t, -r, p0));",
+     "const float t = fmaf(-p0, sc, v);\n        const uint8_t got_signed = code_of(fmaf(t, r, p0));"),
+])
+def test_fma_quotient_check_catches_signed_form_mistakes(plant):
+    """The signed form (quot_signed) is checked on the same pairs; a dropped
+    correction or the abs-form residual applied to signed values must be
+    reported."""
+    old, new = plant
+    src = open(SRC).read()
+    assert old in src
+    src = src.replace(old, new)
+    with tempfile.TemporaryDirectory() as tmp:
+        planted = os.path.join(tmp, "planted.c")
+        open(planted, "w").write(src)
+        exe = os.path.join(tmp, "planted")
+        subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-o", exe, planted, ORACLE_C, "-lm"],
+                       check=True)
+        r = subprocess.run([exe, "64", "3"], capture_output=True, text=True)
+        assert r.returncode == 1 and " mismatches 0" not in r.stdout, r.stdout
