@@ -204,10 +204,10 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
       }
     }
     // y = bf16(xn * bf16(1 + s)); out = bf16(y + shift), two values per
-    // conversion.  The row's largest |out| is kept as two bf16 magnitudes
-    // (an unsigned 16-bit maximum orders non-negative bf16, NaN largest).
+    // conversion.  The row's largest |out| as the quantisation takes it
+    // (NaNs passed over, as fmaxf does).
     u32x4_t o[VPL];
-    u16x2_t mx = {0, 0};
+    float m = 0.0f;
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
 #pragma unroll
@@ -215,13 +215,13 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
         const uint32_t y = pack_bf16x2_once(bf_lo(xn[j][p]) * s1[j][2 * p],
                                             bf_hi(xn[j][p]) * s1[j][2 * p + 1]);
         o[j][p] = pack_bf16x2_once(bf_lo(y) + sh[j][2 * p], bf_hi(y) + sh[j][2 * p + 1]);
-        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, o[j][p] & 0x7fff7fffu));
+        if (QUANT) m = max3_abs(m, bf_lo(o[j][p]), bf_hi(o[j][p]));
       }
       const int64_t c = lane + 64 * j;
       if (WRITE_OUT && c < nchunk && l0 + r < L) *(u32x4_t*)(out + row[r] * D + c * 8) = o[j];
     }
     if (QUANT) {
-      const float amax = wave_max_abs(fmaxf(bf2f(mx[0]), bf2f(mx[1])));
+      const float amax = wave_max_abs(m);
       const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
@@ -232,6 +232,166 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
       }
       if (lane == 0 && l0 + r < L) row_scale[row[r]] = amax / 448.0f;
     }
+  }
+}
+
+// One row per wavefront, for workgroups whose four rows belong to one batch
+// element (B == 1, or L a multiple of 4): the modulation vectors
+// (bf16(1 + scale) and shift, and the gate for GATE) are formed once per
+// workgroup, as fp32, in LDS, and each wave reads its chunks' values from
+// there, so a row costs no per-column VALU work beyond its own chain.  Same
+// arithmetic as ln_modulate_vec, bit for bit, with two changes of method:
+// bf16(v / den) takes the division only for values whose y = v * (1/den)
+// lies within 3 ulps of a bf16 rounding tie (y is within 3 ulps of fl(v /
+// den): 1/den and the product are each rounded once), and the codes come
+// from the signed quotient (quot_signed).  D % 8 == 0, D <= 1536.
+constexpr int kRowChunks = 192;  // 1536 / 8
+template <bool WRITE_OUT, bool QUANT, bool GATE>
+__global__ __launch_bounds__(kThreads) void ln_modulate_row(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ shift, uint16_t* __restrict__ out, int64_t B, int64_t L,
+    int64_t D, float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale,
+    const uint16_t* __restrict__ gate, const uint16_t* __restrict__ res,
+    uint16_t* __restrict__ x1_out) {
+  constexpr int VPL = 3;
+  constexpr int NP = GATE ? 6 : 4;  // s1 lo/hi halves, shift lo/hi, gate lo/hi
+  __shared__ f32x4_t prm[NP][kRowChunks];
+  const int lane = threadIdx.x & 63;
+  const int64_t rows = B * L;
+  const int64_t row0 = (int64_t)blockIdx.x * kWaves;
+  const int64_t rw = row0 + (threadIdx.x >> 6);
+  const bool live = rw < rows;
+  const int64_t row = live ? rw : rows - 1;
+  const int64_t pb = (row0 / L) * D;
+  const int nchunk = (int)(D >> 3);
+  // The row (and residual) loads go first; they are in flight while the
+  // parameters are formed.
+  u32x4_t raw[VPL], rraw[VPL];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int cc = min(lane + 64 * j, nchunk - 1);
+    raw[j] = *(const u32x4_t*)(x + row * D + cc * 8);
+    if (GATE) rraw[j] = *(const u32x4_t*)(res + row * D + cc * 8);
+  }
+  if ((int)threadIdx.x < nchunk) {
+    const int c = threadIdx.x;
+    const u32x4_t sc = *(const u32x4_t*)(scale + pb + c * 8);
+    const u32x4_t sh = *(const u32x4_t*)(shift + pb + c * 8);
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = pack_bf16x2_once(1.0f + bf_lo(sc[i]), 1.0f + bf_hi(sc[i]));
+      f[2 * i] = bf_lo(w);
+      f[2 * i + 1] = bf_hi(w);
+    }
+    prm[0][c] = f32x4_t{f[0], f[1], f[2], f[3]};
+    prm[1][c] = f32x4_t{f[4], f[5], f[6], f[7]};
+    unpack8(sh, f);
+    prm[2][c] = f32x4_t{f[0], f[1], f[2], f[3]};
+    prm[3][c] = f32x4_t{f[4], f[5], f[6], f[7]};
+    if (GATE) {
+      unpack8(*(const u32x4_t*)(gate + pb + c * 8), f);
+      prm[NP - 2][c] = f32x4_t{f[0], f[1], f[2], f[3]};
+      prm[NP - 1][c] = f32x4_t{f[4], f[5], f[6], f[7]};
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  // Every bf16 rounding of the chain is one rbf16 (the value stays fp32).
+  float v[VPL][8];
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    unpack8(raw[j], v[j]);
+    if (GATE) {
+      // x1 = bf16(x + bf16(gate * res)), written out, normalised below.
+      const int cc = min(lane + 64 * j, nchunk - 1);
+      const f32x4_t g0 = prm[NP - 2][cc], g1 = prm[NP - 1][cc];
+      const float g[8] = {g0[0], g0[1], g0[2], g0[3], g1[0], g1[1], g1[2], g1[3]};
+      float r[8];
+      unpack8(rraw[j], r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = rbf16(v[j][e] + rbf16(g[e] * r[e]));
+      if (lane + 64 * j < nchunk) *(u32x4_t*)(x1_out + row * D + (lane + 64 * j) * 8) = pack8(v[j]);
+    }
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    float cs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) cs += v[j][e];
+    sum += lane + 64 * j < nchunk ? cs : 0.0f;
+  }
+  const float mean = wave_sum(sum) / (float)D;
+  float sq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    float cs = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[j][e] -= mean;
+      cs = __builtin_fmaf(v[j][e], v[j][e], cs);
+    }
+    sq += lane + 64 * j < nchunk ? cs : 0.0f;
+  }
+  const float den = sqrtf(wave_sum(sq) / (float)D + eps);
+  const float rd = 1.0f / den;
+  // xn = bf16(v / den) from y = v * (1/den): y lies within 3 ulps of
+  // fl(v / den) (1/den and the product are each rounded once), so their bf16
+  // roundings agree unless y's low 16 bits are within 3 of the tie 0x8000,
+  // i.e. (bits + 0x8003) mod 2^16 <= 6.  The lane keeps the smallest such
+  // distance; values near a tie (rare) and rows failing ln_fast_ok divide.
+  const bool fast = ln_fast_ok(mean, rd);
+  float xn[VPL][8];
+  uint16_t near = fast ? (uint16_t)0xffff : (uint16_t)0;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float y = v[j][e] * rd;
+      xn[j][e] = rbf16(y);
+      near = min(near, (uint16_t)(__float_as_uint(y) + 0x8003u));
+    }
+  if (__builtin_amdgcn_ballot_w64(near <= 6)) {
+#pragma unroll
+    for (int j = 0; j < VPL; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = v[j][e] * rd;
+        if (!fast || (uint16_t)(__float_as_uint(y) + 0x8003u) <= 6) xn[j][e] = rbf16(v[j][e] / den);
+      }
+  }
+  // o = bf16(bf16(xn * bf16(1 + s)) + shift); the row's largest |o|.
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < VPL; ++j) {
+    const int cc = min(lane + 64 * j, nchunk - 1);
+    const f32x4_t sa = prm[0][cc], sb = prm[1][cc], ha = prm[2][cc], hb = prm[3][cc];
+    const float s1[8] = {sa[0], sa[1], sa[2], sa[3], sb[0], sb[1], sb[2], sb[3]};
+    const float sh[8] = {ha[0], ha[1], ha[2], ha[3], hb[0], hb[1], hb[2], hb[3]};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xn[j][e] = rbf16(rbf16(xn[j][e] * s1[e]) + sh[e]);
+    // a repeated chunk (past the row's end) changes no maximum
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) m = max3_abs(m, xn[j][e], xn[j][e + 1]);
+    if (WRITE_OUT && lane + 64 * j < nchunk)
+      *(u32x4_t*)(out + row * D + (lane + 64 * j) * 8) = pack8(xn[j]);
+  }
+  if (QUANT) {
+    const float amax = wave_max_abs(m);
+    const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
+    const float qsf = fminf(qs, 3.40282347e38f);
+#pragma unroll
+    for (int j = 0; j < VPL; ++j) {
+      const float* o = xn[j];
+      u32x2_t q;
+      q[0] = e4m3x4(quot_signed(o[0], qr, qsf), quot_signed(o[1], qr, qsf),
+                    quot_signed(o[2], qr, qsf), quot_signed(o[3], qr, qsf));
+      q[1] = e4m3x4(quot_signed(o[4], qr, qsf), quot_signed(o[5], qr, qsf),
+                    quot_signed(o[6], qr, qsf), quot_signed(o[7], qr, qsf));
+      if (lane + 64 * j < nchunk) *(u32x2_t*)(codes + row * D + (lane + 64 * j) * 8) = q;
+    }
+    if (lane == 0) row_scale[row] = amax / 448.0f;
   }
 }
 
@@ -364,7 +524,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_vec(
     }
     const float rstd = rsqrtf(wave_sum(sq) / (float)D + eps);
     u32x4_t o[VPL];
-    u16x2_t mx = {0, 0};
+    float m = 0.0f;  // the row's largest |y|, NaNs passed over as fmaxf does
 #pragma unroll
     for (int j = 0; j < VPL; ++j) {
 #pragma unroll
@@ -373,13 +533,13 @@ __global__ __launch_bounds__(kThreads) void layer_norm_vec(
         const float y1 =
             __builtin_fmaf(bf_hi(wraw[j][p]), v[r][j][2 * p + 1] * rstd, bf_hi(braw[j][p]));
         o[j][p] = pack_bf16x2_once(y0, y1);
-        mx = __builtin_elementwise_max(mx, __builtin_bit_cast(u16x2_t, o[j][p] & 0x7fff7fffu));
+        if (QUANT) m = max3_abs(m, bf_lo(o[j][p]), bf_hi(o[j][p]));
       }
       const int64_t c = lane + 64 * j;
       if (WRITE_OUT && c < nchunk && r0 + r < rows) *(u32x4_t*)(out + row[r] * D + c * 8) = o[j];
     }
     if (QUANT) {
-      const float amax = wave_max_abs(fmaxf(bf2f(mx[0]), bf2f(mx[1])));
+      const float amax = wave_max_abs(m);
       const float qs = fmaxf(amax, 1e-12f) / 448.0f, qr = 1.0f / qs;
 #pragma unroll
       for (int j = 0; j < VPL; ++j) {
@@ -493,7 +653,20 @@ extern "C" int fvsr_ln_modulate(const void* x, const void* scale, const void* sh
   uint8_t* qp = (uint8_t*)codes;
   const bool vec = D % 8 == 0 && D <= 512 * 3 && aligned16(x) && aligned16(scale) &&
                    aligned16(shift) && (!out || aligned16(out)) && (!codes || aligned16(codes));
-  if (vec) {
+  if (vec && (B == 1 || L % kWaves == 0)) {
+    // one row per wave, the workgroup's modulation vectors in LDS
+    const uint16_t* none = nullptr;
+    uint16_t* none_out = nullptr;
+    if (out && codes)
+      hipLaunchKernelGGL((ln_modulate_row<true, true, false>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, none, none, none_out);
+    else if (out)
+      hipLaunchKernelGGL((ln_modulate_row<true, false, false>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, none, none, none_out);
+    else
+      hipLaunchKernelGGL((ln_modulate_row<false, true, false>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, none, none, none_out);
+  } else if (vec) {
     const int64_t groups = B * ((L + kLnRows - 1) / kLnRows);
     const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves));
     if (out && codes)
@@ -563,8 +736,23 @@ extern "C" int fvsr_gate_add_ln_modulate(const void* x, const void* gate, const 
                  *rp = (const uint16_t*)res;
   uint16_t *op = (uint16_t*)out, *x1p = (uint16_t*)x1;
   uint8_t* qp = (uint8_t*)codes;
+  const dim3 block(kThreads);
+  if (B == 1 || L % kWaves == 0) {
+    // one row per wave, the workgroup's modulation vectors and gate in LDS
+    const dim3 grid((unsigned)((B * L + kWaves - 1) / kWaves));
+    if (out && codes)
+      hipLaunchKernelGGL((ln_modulate_row<true, true, true>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, gp, rp, x1p);
+    else if (out)
+      hipLaunchKernelGGL((ln_modulate_row<true, false, true>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, gp, rp, x1p);
+    else
+      hipLaunchKernelGGL((ln_modulate_row<false, true, true>), grid, block, 0, st, xp, sp, hp, op,
+                         B, L, D, eps, qp, row_scale, gp, rp, x1p);
+    return fvsr_launch_status();
+  }
   const int64_t groups = B * ((L + kLnRows - 1) / kLnRows);
-  const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves)), block(kThreads);
+  const dim3 vgrid((unsigned)((groups + kWaves - 1) / kWaves));
   if (out && codes)
     hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, true, true, true>), vgrid, block, 0, st, xp, sp,
                        hp, op, B, L, D, eps, qp, row_scale, gp, rp, x1p);

@@ -33,6 +33,15 @@ FVSR_DEV uint32_t pack_bf16x2(float a, float b) {
 }
 // fp32 -> bf16 -> fp32 (the "round-trip through bf16" of eager).
 FVSR_DEV float round_bf16(float a) { return bf_lo(pack_bf16x2(a, 0.0f)); }
+// The same round trip in one instruction: bf16(a) converted into the high
+// half with +0 in the low half is the fp32 bit pattern of bf16(a).  (Written
+// out: the compiler would otherwise merge two of these into one conversion
+// plus byte permutes.)
+FVSR_DEV float rbf16(float a) {
+  float r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
 
 // Four fp32 (of magnitude below 464) -> four e4m3fn codes in one dword.
 FVSR_DEV uint32_t pack_e4m3x4(float a, float b, float c, float d) {
@@ -154,6 +163,15 @@ FVSR_DEV uint32_t e4m3x4(float a, float b, float c, float d) {
   return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
 }
 
+// max(m, |a|, |b|) in one v_max3_f32.  A NaN operand is passed over as
+// fmaxf does (the kernels' NaNs are quiet: bf16 data and conversions), and
+// the operands need no canonicalising maximum first.
+FVSR_DEV float max3_abs(float m, float a, float b) {
+  float r;
+  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+  return r;
+}
+
 // Packed bf16 pair -> the two floats.
 FVSR_DEV float lo_f(uint32_t p) { return __uint_as_float(p << 16); }
 FVSR_DEV float hi_f(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
@@ -181,7 +199,9 @@ FVSR_DEV float quot_abs(float v, float r, float sc) {
 // the result is -quot(|v|) for negative v, and equals quot_abs's value for
 // v > 0 (t is exactly -e, or both are +0).  For v = -0 it is -0 (q0 = -0,
 // t = +0, -0 - 0 = -0), so the conversion's own sign gives the code.  Checked
-// over the same pairs, both signs, by tests/native/fma_quotient_check.c.
+// over the same pairs, both signs, by tests/native/fma_quotient_check.c.  (A
+// NaN's sign may come out either way; v_cvt_pk_fp8_f32 writes 0xFF for every
+// NaN in any case.)
 FVSR_DEV float quot_signed(float v, float r, float sc) {
   const float q0 = v * r;
   const float t = fmaf(q0, sc, -v);

@@ -129,14 +129,6 @@ FVSR_DEV void load_row(u32x4_t (&v)[VPL], const uint16_t* x, int64_t row, int64_
   }
 }
 
-// max(m, |a|, |b|) in one v_max3_f32.  The table holds quiet NaNs only (the
-// GELU of a NaN input), which v_max3_f32 passes over as fmaxf does, and the
-// operands need no canonicalising maximum first.
-FVSR_DEV float max3_abs(float m, float a, float b) {
-  float r;
-  asm("v_max3_f32 %0, %1, |%2|, |%3|" : "=v"(r) : "v"(m), "v"(a), "v"(b));
-  return r;
-}
 
 // Row `row` is in v (bf16).  Its GELU values are looked up straight into fp32
 // registers (the bf16 result shifted into the high half: one operation per

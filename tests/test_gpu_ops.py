@@ -373,7 +373,11 @@ def test_gemm_gate_add_epilogue(ops, MNK):
 
 # ----------------------------------------------------------------------------- AdaLN
 
-@pytest.mark.parametrize("BLD", [(1, 16896, 1536), (2, 37, 1536), (2, 5, 100), (1, 3, 2048)])
+# one row per wave with the modulation vectors in LDS (B == 1 or L % 4 == 0;
+# a partial last workgroup; D below 1536), two rows per wave (L % 4 != 0),
+# and the generic kernel (D % 8 != 0, D > 1536)
+@pytest.mark.parametrize("BLD", [(1, 16896, 1536), (2, 36, 1536), (1, 4226, 1536), (1, 9, 512),
+                                 (2, 37, 1536), (2, 5, 100), (1, 3, 2048)])
 def test_ln_modulate(ops, BLD):
     B, L, D = BLD
     x = rnd_bits(BLD, seed=L)
@@ -390,6 +394,50 @@ def test_ln_modulate(ops, BLD):
     assert np.array_equal(host_f(s).reshape(-1), rs)
     q2, s2 = ops.fused_ln_modulate_quant(xd, scd, shd, eps=1e-6)
     assert np.array_equal(host_codes(q2), rq)
+
+
+def _codes_equal_nan(got, ref):
+    """Codes equal, except that a NaN's code may carry either sign: the
+    device's conversion writes 0xFF for every NaN, the oracle (torch's
+    conversion) keeps the NaN's sign (0x7F or 0xFF)."""
+    nan = (ref & 0x7F) == 0x7F
+    assert np.array_equal(got[~nan], ref[~nan])
+    assert ((got[nan] & 0x7F) == 0x7F).all()
+
+
+@pytest.mark.parametrize("B,L", [(1, 64), (2, 37)])
+def test_ln_modulate_quant_special_rows(ops, B, L):
+    """Rows that leave the fast path or stress it: NaN and inf entries, a
+    constant row (zero variance), a zero row, values near the smallest
+    normals (the division path) and large ones, in the one-row-per-wave
+    kernel (B = 1) and the two-rows-per-wave one (L % 4 != 0).  Codes and
+    scales must be the oracle's quantisation of the device's own bf16 rows,
+    whose row maximum passes NaNs over (the oracle's and fmaxf's rule); the
+    finite rows agree with the oracle's LN + modulate."""
+    D = 1536
+    x = rnd_bits((B, L, D), seed=7)
+    x[0, 0, ::7] = 0x7FC0                     # NaNs
+    x[0, 1, ::11] = 0x7F80                    # +inf
+    x[0, 1, 5] = 0xFF80                       # -inf
+    x[0, 2, :] = O.bf16_bits(np.float32(1.5))  # constant row
+    x[0, 3, :] = 0                            # zero row
+    x[0, 4] = O.bf16_bits(O.from_bf16_bits(x[0, 4]) * np.float32(2.0 ** -120))
+    x[0, 5] = O.bf16_bits(O.from_bf16_bits(x[0, 5]) * np.float32(2.0 ** 100))
+    sc = rnd_bits((B, 1, D), seed=8, scale=0.1)
+    sh = rnd_bits((B, 1, D), seed=9, scale=0.1)
+    sh[0, 0, :16] = 0x8000                    # -0 shifts
+    q, s, out = ops.fused_ln_modulate_quant(dev_bf16(x), dev_bf16(sc), dev_bf16(sh), eps=1e-6,
+                                            write_bf16=True)
+    ob = host_bits(out).reshape(B * L, D)
+    rq, rs = O.quantize_fp8(ob, per_row=True)
+    _codes_equal_nan(host_codes(q), rq)
+    assert np.array_equal(host_f(s).reshape(-1), rs, equal_nan=True)
+    ref = O.ln_modulate(O.from_bf16_bits(x), O.from_bf16_bits(sc), O.from_bf16_bits(sh), 1e-6)
+    got = host_f(out)
+    fin = np.isfinite(ref).all(axis=-1)
+    assert fin[0, 2:].all()
+    _close_bf16(got[fin], ref[fin], max_abs=0.03125)
+    assert np.isnan(got[0, 0]).all() == np.isnan(ref[0, 0]).all()
 
 
 def test_ln_modulate_golden(ops):
