@@ -6,6 +6,11 @@
 // swap costs nothing.  The (cos, sin) table is read in its interleaved
 // [L, head_dim/2, 2] fp32 layout — the view_as_real of the complex freqs_cis —
 // as two 16-byte loads per chunk.
+//
+// Products and sums are contracted into fmas only where written out (the
+// sum of squares and the rotation), so the results do not depend on the
+// compiler's choices.
+#pragma clang fp contract(off)
 #include "common.h"
 
 namespace {
@@ -30,7 +35,7 @@ FVSR_DEV void rms_rope_row(const uint16_t* xr, const uint16_t* __restrict__ w,
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float a = bf_lo(v[j][i]), b = bf_hi(v[j][i]);
-      sq += in ? a * a + b * b : 0.0f;
+      sq = in ? __builtin_fmaf(b, b, __builtin_fmaf(a, a, sq)) : sq;
     }
   }
   // Weights and (cos, sin) for every chunk, loaded before the reduction
@@ -54,12 +59,12 @@ FVSR_DEV void rms_rope_row(const uint16_t* xr, const uint16_t* __restrict__ w,
     u32x4_t o;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float ye = round_bf16(bf_lo(v[j][i]) * r) * bf_lo(wv[j][i]);
-      const float yo = round_bf16(bf_hi(v[j][i]) * r) * bf_hi(wv[j][i]);
+      const float ye = rbf16(bf_lo(v[j][i]) * r) * bf_lo(wv[j][i]);
+      const float yo = rbf16(bf_hi(v[j][i]) * r) * bf_hi(wv[j][i]);
       if (ROPE) {
         const float cc = i < 2 ? cs0[j][2 * i] : cs1[j][2 * (i - 2)];
         const float ss = i < 2 ? cs0[j][2 * i + 1] : cs1[j][2 * (i - 2) + 1];
-        o[i] = pack_bf16x2(ye * cc - yo * ss, ye * ss + yo * cc);
+        o[i] = pack_bf16x2(__builtin_fmaf(ye, cc, -(yo * ss)), __builtin_fmaf(ye, ss, yo * cc));
       } else {
         o[i] = pack_bf16x2(ye, yo);
       }
@@ -145,19 +150,20 @@ __global__ __launch_bounds__(kThreads) void rms_rope_generic(
   float sq = 0.0f;
   for (int64_t d = lane; d < D; d += 64) {
     const float a = bf2f(xr[d]);
-    sq += a * a;
+    sq = __builtin_fmaf(a, a, sq);
   }
   const float r = rsqrtf(wave_sum(sq) / (float)D + eps);
   const int64_t s = row % L;
   for (int64_t d = lane; d < D; d += 64) {
-    const float y = round_bf16(bf2f(xr[d]) * r) * bf2f(w[d]);
+    const float y = rbf16(bf2f(xr[d]) * r) * bf2f(w[d]);
     float o = y;
     if (rope) {
       const int64_t dp = d ^ 1;
-      const float yp = round_bf16(bf2f(xr[dp]) * r) * bf2f(w[dp]);
+      const float yp = rbf16(bf2f(xr[dp]) * r) * bf2f(w[dp]);
       const int64_t i = (d % head_dim) >> 1;
       const float cc = cs[(s * (head_dim >> 1) + i) * 2], ss = cs[(s * (head_dim >> 1) + i) * 2 + 1];
-      o = (d & 1) ? (yp * ss + y * cc) : (y * cc - yp * ss);
+      // the same expressions as the vector kernel (ye, yo = even, odd)
+      o = (d & 1) ? __builtin_fmaf(yp, ss, y * cc) : __builtin_fmaf(y, cc, -(yp * ss));
     }
     out[row * D + d] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffff);
   }
