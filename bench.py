@@ -169,6 +169,38 @@ def timeit(torch, fn, n_sets, iters=20, warmup=3):
     return e0.elapsed_time(e1) / iters
 
 
+def gtime(torch, fn, n_sets, iters=20, replays=3):
+    """Device-only ms per call: `iters` calls (cycling through the input sets)
+    captured in one HIP graph and replayed, so no host work sits between the
+    kernels (the ops used here allocate nothing outside torch's graph pool and
+    issue no memsets).  None if the capture fails."""
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(3):
+                fn(i % n_sets)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(iters):
+                fn(i % n_sets)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del graph
+        return e0.elapsed_time(e1) / (replays * iters)
+    except Exception as exc:  # a capture problem must not end the bench
+        print(f"[bench] graph timing unavailable: {exc}", file=sys.stderr, flush=True)
+        return None
+
+
 def n_sets_for(bytes_per_set, target=640e6):
     return max(2, int(math.ceil(target / bytes_per_set)))
 
@@ -200,9 +232,14 @@ def components(torch, fv):
     q = [fv.quantize_fp8(x, per_token=True) for x in xs]
     t_q = timeit(torch, lambda i: fv.quantize_fp8(xs[i], per_token=True), ns)
     t_g = timeit(torch, lambda i: fv.fp8_gemm(q[i][0], q[i][1], w8, ws, bias), ns)
+    k_q = gtime(torch, lambda i: fv.quantize_fp8(xs[i], per_token=True), ns)
+    k_g = gtime(torch, lambda i: fv.fp8_gemm(q[i][0], q[i][1], w8, ws, bias), ns)
     qbytes = M * K * 3 + M * 4
     out["C1_fp8_linear"] = {
         "quant_ms": t_q, "quant_GBps": gbs(qbytes, t_q), "quant_frac_hbm": gbs(qbytes, t_q) * 1e9 / PEAK["hbm"],
+        "quant_kernel_ms": k_q,
+        "quant_kernel_frac_hbm": gbs(qbytes, k_q) * 1e9 / PEAK["hbm"] if k_q else None,
+        "gemm_kernel_ms": k_g,
         "gemm_ms": t_g, "gemm_TFLOPs": 2 * M * N * K / (t_g * 1e-3) / 1e12,
         "gemm_frac_fp8": 2 * M * N * K / (t_g * 1e-3) / PEAK["fp8"]}
     del xs, q
@@ -217,7 +254,10 @@ def components(torch, fv):
         (1 + 0.1 * torch.randn(DIM, device=dev, generator=g)).to(torch.bfloat16)
     fc = wan_freqs_cis(2, 48, 88, device=dev)
     t = timeit(torch, lambda i: fv.fused_rms_rope_qk(qs[i], ks[i], wq, wk, fc), ns)
+    kt = gtime(torch, lambda i: fv.fused_rms_rope_qk(qs[i], ks[i], wq, wk, fc), ns)
     out["C2_rms_rope_qk"] = {"ms": t, "GBps": gbs(nbytes, t), "frac_hbm": gbs(nbytes, t) * 1e9 / PEAK["hbm"],
+                             "kernel_ms": kt,
+                             "kernel_frac_hbm": gbs(nbytes, kt) * 1e9 / PEAK["hbm"] if kt else None,
                              "algorithmic_MB": nbytes / 1e6}
     del qs, ks
 
@@ -247,6 +287,7 @@ def components(torch, fv):
     t_rq = timeit(torch, lambda i: fv.fused_gelu_quant_fp8(hs_[i % nh], per_token=True), nh)
     rq_bytes = M3 * FFN * 3 + M3 * 4
     hqs = [fv.fused_gelu_quant_fp8(hs_[i], per_token=True) for i in range(min(nh, 5))]
+    hqs_src = hs_[:3]
     del hs_
     nq = len(hqs)
     res = xs[0].view(M3, DIM)
@@ -264,6 +305,16 @@ def components(torch, fv):
     t_ffn = timeit(torch, lambda i: (lambda h8: fv.fp8_gemm(h8[0], h8[1], w2, s2, b2))(
         gemm_gelu_quant_fp8(x8s[i % nx][0], x8s[i % nx][1], lin1, True)), nx)
     fl = 2 * M3 * DIM * FFN
+    # device-only times of the row kernels (graph replays, no host work)
+    k3 = {"ln_modulate_quant": (gtime(torch, lambda i: fv.fused_ln_modulate_quant(xs[i], sc, sh), ns),
+                                ln_bytes),
+          "gelu_quant": (gtime(torch, lambda i: fv.fused_gelu_quant_fp8(hqs_src[i % len(hqs_src)],
+                                                                        per_token=True),
+                               len(hqs_src)), rq_bytes),
+          "gate_add": (gtime(torch, lambda i: fv.fused_gate_add(xs[i], gt, xs[(i + 1) % ns]), ns),
+                       ga_bytes),
+          "gate_add_ln_modulate_quant": (gtime(torch, lambda i: fused_gate_add_ln_modulate_quant(
+              xs[i], gt, xs[(i + 1) % ns], sc, sh), ns), gal_bytes)}
     out["C3_adaln_fp8_ffn"] = {
         "ln_modulate_quant_ms": t_ln, "ln_modulate_quant_GBps": gbs(ln_bytes, t_ln),
         "ln_modulate_quant_frac_hbm": gbs(ln_bytes, t_ln) * 1e9 / PEAK["hbm"],
@@ -274,13 +325,21 @@ def components(torch, fv):
         "gemm_ffn2_ms": t_g2, "gemm_ffn2_TFLOPs": fl / (t_g2 * 1e-3) / 1e12,
         "gemm_ffn2_frac_fp8": fl / (t_g2 * 1e-3) / PEAK["fp8"],
         "gemm_ffn2_gate_epilogue_ms": t_g2g,
+        "gemm_ffn0_kernel_ms": gtime(torch, lambda i: fv.fp8_gemm(
+            x8s[i % nx][0], x8s[i % nx][1], w1, s1, b1, out=hb), nx),
+        "gemm_ffn2_kernel_ms": gtime(torch, lambda i: fv.fp8_gemm(
+            hqs[i % nq][0], hqs[i % nq][1], w2, s2, b2, out=o2), nq),
         "gate_add_ms": t_ga, "gate_add_GBps": gbs(ga_bytes, t_ga),
         "gate_add_frac_hbm": gbs(ga_bytes, t_ga) * 1e9 / PEAK["hbm"],
         "gate_add_ln_modulate_quant_ms": t_gal,
         "gate_add_ln_modulate_quant_GBps": gbs(gal_bytes, t_gal),
         "gate_add_ln_modulate_quant_frac_hbm": gbs(gal_bytes, t_gal) * 1e9 / PEAK["hbm"],
         "ffn_chain_ms": t_ffn}
-    del xs, x8s, hqs, hb
+    for name, (kt, nb) in k3.items():
+        out["C3_adaln_fp8_ffn"][name + "_kernel_ms"] = kt
+        out["C3_adaln_fp8_ffn"][name + "_kernel_frac_hbm"] = (gbs(nb, kt) * 1e9 / PEAK["hbm"]
+                                                              if kt else None)
+    del xs, x8s, hqs, hb, hqs_src
 
     # C4: block-sparse attention [1,12,16896,128], C4 mask, plus a density sweep;
     # q/k/v rotated over 4 sets (623 MB > the 256 MB MALL).
@@ -290,6 +349,7 @@ def components(torch, fv):
     keep = window_plus_random_mask(device=dev)
     kept = int(keep.sum().item())
     t4 = timeit(torch, lambda i: block_sparse_attention_bhsd(*qkvs[i], keep), ns4, iters=12)
+    k4 = gtime(torch, lambda i: block_sparse_attention_bhsd(*qkvs[i], keep), ns4, iters=12)
     fl4 = 4 * 128 ** 3 * kept
     sweep = []
     from flashvsr_sm89_ops.lcsa.masks import density_mask
@@ -301,6 +361,8 @@ def components(torch, fv):
                       "TFLOPs": 4 * 128 ** 3 * kk / (td * 1e-3) / 1e12})
     out["C4_bsa"] = {"ms_per_layer": t4, "density": kept / (HEADS * 132 * 132), "input_sets": ns4,
                      "TFLOPs": fl4 / (t4 * 1e-3) / 1e12, "frac_bf16": fl4 / (t4 * 1e-3) / PEAK["bf16"],
+                     "kernel_ms": k4,
+                     "kernel_frac_bf16": fl4 / (k4 * 1e-3) / PEAK["bf16"] if k4 else None,
                      "density_sweep": sweep}
     del qkv, qkvs
 
@@ -321,16 +383,17 @@ def components(torch, fv):
     Ld = _lib.lib()
     wn = Ld.fvsr_draft_workspace_floats(HEADS, HD, NB, NB)
     wsd = torch.empty(wn, dtype=torch.float32, device=dev)
-    st = _lib.stream(wsd)
 
     def draft(i):
+        st = _lib.stream(wsd)  # the current stream at call time (graph capture uses its own)
         _lib.check(Ld.fvsr_draft_block_mask(
             qd[i].data_ptr(), DIM, tm.data_ptr(), kd[i].data_ptr(), DIM, tm.data_ptr(), HEADS, HD,
             NB, NB, 2, loc.data_ptr(), 66, 66, topk, None, sel.data_ptr(), cnt.data_ptr(),
             wsd.data_ptr(), wn, st), "draft")
     t_d = timeit(torch, draft, ns, iters=50)
+    k_d = gtime(torch, draft, ns, iters=50)
     pool_bytes = 2 * L * DIM * 2
-    out["F1_draft_index"] = {"ms": t_d, "pool_MB": pool_bytes / 1e6,
+    out["F1_draft_index"] = {"ms": t_d, "kernel_ms": k_d, "pool_MB": pool_bytes / 1e6,
                              "GBps_pool_bytes": gbs(pool_bytes, t_d),
                              "kept_frac": float(cnt.sum().item()) / (HEADS * NB * NB)}
     del qd, kd
