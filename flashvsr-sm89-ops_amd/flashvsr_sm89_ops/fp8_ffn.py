@@ -35,8 +35,8 @@ def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
     if y2.numel() and y2.stride(1) != 1:
         y2 = y2.contiguous()
     x8 = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=y2.device)
-    s = (torch.empty((M, 1), dtype=torch.float32, device=y2.device) if per_token
-         else torch.zeros(1, dtype=torch.float32, device=y2.device))
+    alloc = torch.zeros if y2.numel() == 0 else torch.empty  # the kernels write every scale
+    s = alloc((M, 1) if per_token else (1,), dtype=torch.float32, device=y2.device)
     if y2.numel() == 0:
         return x8, s
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
@@ -61,7 +61,8 @@ def gemm_gelu_quant_fp8(x8: torch.Tensor, s: torch.Tensor, lin, per_token: bool)
     h = fp8_gemm(x8, s, lin.weight, lin.w_scale, lin.bias, epilogue=_lib.EPI_ROWMAX,
                  amax_part=hmax)
     h8 = torch.empty((M, N), dtype=torch.float8_e4m3fn, device=x8.device)
-    hs = torch.zeros(1, dtype=torch.float32, device=x8.device)
+    hs = (torch.zeros if M == 0 or N == 0 else torch.empty)(1, dtype=torch.float32,
+                                                             device=x8.device)
     ws = torch.empty(2 * int(_lib.lib().fvsr_quant_workspace_floats(M, N, 0)), dtype=torch.float32,
                      device=x8.device)
     _lib.check(_lib.lib().fvsr_gelu_quant_fp8_tensor(h.data_ptr(), M, N, hmax.data_ptr(), nparts,

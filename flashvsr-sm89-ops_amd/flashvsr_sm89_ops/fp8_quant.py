@@ -33,10 +33,9 @@ def quantize_fp8(x2: torch.Tensor, per_token: bool = False):
     if x2.numel() and x2.stride(1) != 1:
         x2 = x2.contiguous()
     q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x2.device)
-    if per_token:
-        s = torch.empty((M, 1), dtype=torch.float32, device=x2.device)
-    else:
-        s = torch.zeros(1, dtype=torch.float32, device=x2.device)
+    # The kernels write every scale; only an empty input keeps amax = 0.
+    alloc = torch.zeros if x2.numel() == 0 else torch.empty
+    s = alloc((M, 1) if per_token else (1,), dtype=torch.float32, device=x2.device)
     if x2.numel() == 0:
         return q, s
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR

@@ -33,6 +33,8 @@ def _rows(x: torch.Tensor, name: str):
 def _local_u8(local: torch.Tensor, device) -> torch.Tensor:
     if local.dim() != 2:
         raise ValueError(f"local mask must be [sq, sk], got {tuple(local.shape)}")
+    if local.dtype == torch.bool and local.device == torch.device(device):
+        return local.contiguous().view(torch.uint8)  # same bytes: no conversion kernel
     return local.to(device=device, dtype=torch.uint8).contiguous()
 
 

@@ -34,7 +34,9 @@ def build_csr(keep: torch.Tensor):
     the host."""
     _lib.require_gpu(keep)
     H, NQ, NK = keep.shape
-    k8 = keep.to(torch.uint8).contiguous()
+    # a bool mask is already one byte per entry: no conversion kernel
+    k8 = (keep.contiguous().view(torch.uint8) if keep.dtype == torch.bool
+          else keep.to(torch.uint8).contiguous())
     sel = torch.empty((H, NQ, max(NK, 1)), dtype=torch.int32, device=keep.device)
     cnt = torch.empty((H, NQ), dtype=torch.int32, device=keep.device)
     _lib.check(_lib.lib().fvsr_block_index(k8.data_ptr(), H, NQ, NK, sel.data_ptr(),
