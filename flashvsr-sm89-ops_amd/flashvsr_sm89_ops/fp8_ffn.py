@@ -40,7 +40,7 @@ def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
     if y2.numel() == 0:
         return x8, s
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
-    ws = _workspace(y2, M, K, mode)
+    ws = None if per_token else _workspace(y2, M, K, mode)  # per-row scales need none
     _lib.check(_lib.lib().fvsr_quant_fp8(y2.data_ptr(), M, K, y2.stride(0), mode, 1,
                                          x8.data_ptr(), s.data_ptr(), _lib.ptr(ws),
                                          0 if ws is None else ws.numel(), _lib.stream(y2)),

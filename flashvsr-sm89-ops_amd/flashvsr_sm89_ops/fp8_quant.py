@@ -39,7 +39,7 @@ def quantize_fp8(x2: torch.Tensor, per_token: bool = False):
     if x2.numel() == 0:
         return q, s
     mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
-    ws = _workspace(x2, M, K, mode)
+    ws = None if per_token else _workspace(x2, M, K, mode)  # per-row scales need none
     _lib.check(_lib.lib().fvsr_quant_fp8(x2.data_ptr(), M, K, x2.stride(0), mode, 0,
                                          q.data_ptr(), s.data_ptr(), _lib.ptr(ws),
                                          0 if ws is None else ws.numel(), _lib.stream(x2)),
