@@ -36,12 +36,14 @@ FVSR_DEV double wave_sum_f64(double v) {
 // avg[n][c] for the NQ query blocks (blockIdx.x < NQ) and the NK key blocks
 // (the rest): token j of block n is row map[n*128 + j] (n*128 + j without a
 // map), rows ts elements apart.  A workgroup covers 512 channels of one block:
-// lane g owns 8 channels, wave w adds tokens 32w..32w+31 in two batches of 16
-// (each batch's loads issued before its first add), and the four partial fp64
-// sums meet in LDS.  The (NQ + NK) * ceil(C/512) workgroups fit the
-// GPU in one round at the C5 shape.
-constexpr int kPoolWaves = 4;
-constexpr int kPoolBatch = 16;
+// lane g owns 8 channels, wave w adds tokens 16w..16w+15 in four batches of 4
+// (each batch's loads issued before its first add), and the eight partial
+// fp64 sums meet in LDS.  The (NQ + NK) * ceil(C/512) workgroups fit the GPU
+// in one round at the C5 shape.  Measured at the C5 geometry (whole draft):
+// 4 waves x 2 batches of 16: 52.2 us; 8 x 4 of 4: 47.2; 8 x 2 of 8: 48.1;
+// 8 x 1 of 16: 54.3; 16 waves: 54.5-55.9.
+constexpr int kPoolWaves = 8;
+constexpr int kPoolBatch = 4;
 
 __global__ __launch_bounds__(kPoolWaves * 64) void pool_kernel(
     const uint16_t* __restrict__ q, int64_t qts, const int32_t* __restrict__ qmap,
