@@ -13,6 +13,8 @@ timed region.  ``value`` is ms per DiT layer (block); lower is better.
 Alongside it the JSON line carries
   roofline      the dominant kernel of the step, timed with HIP events on the
                 stream it runs on during the timed steps, against MI355X peak;
+  graph_ms_per_step  the same chunk captured once as a HIP graph and
+                replayed (checked bitwise against the eager output first);
   components    op-level measurements at the other BASELINE configs
                 (C1 FP8 linear, C2 RMSNorm+RoPE, C3 AdaLN + FP8 FFN, C4 BSA),
                 inputs rotated over > 512 MB so the 256 MB MALL cannot serve them;
@@ -134,8 +136,38 @@ def run_stack(args, torch, fv):
     dom_avg = sum(dom_ms) / len(dom_ms)
     log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f}s); "
         f"dominant {dominant}: {dom_avg:.4f} ms avg over {len(dom_ms)} launches")
+    # The same chunk captured once as a HIP graph and replayed (the kernels
+    # are identical; what goes is the host work and launch gaps between them).
+    # Reported beside the eager figure, not as the line's value.
+    graph_ms = None
+    try:
+        xs = x.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            stack(xs, t_mod, cs, index, tmap)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            yg = stack(xs, t_mod, cs, index, tmap)
+        graph.replay()
+        torch.cuda.synchronize()
+        if not torch.equal(yg, y):
+            raise RuntimeError("graph replay differs from the eager chunk")
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        g0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        graph_ms = g0.elapsed_time(g1) / args.steps
+        log(f"graph replay: {graph_ms:.3f} ms/step")
+        del graph, yg, xs
+    except Exception as exc:  # the eager figure stands on its own
+        log(f"graph replay unavailable: {exc}")
     return dict(ms_step=ms_step, per_op=per_op, dominant=dominant, dom_avg=dom_avg,
-                kept=kept, density=kept / (HEADS * 132 * 132))
+                kept=kept, density=kept / (HEADS * 132 * 132), graph_ms=graph_ms)
 
 
 def roofline_for(name, avg_ms, kept):
@@ -718,7 +750,9 @@ def main():
         "config": {"workload": f"C5: {args.blocks}-block FlashVSR-Tiny DiT stack, one chunk @1408x768",
                    "tokens": L, "dim": DIM, "heads": HEADS, "head_dim": HD, "ffn": FFN,
                    "blocks": args.blocks, "bsa_density": r["density"], "scales": "per-token x per-channel"},
-        "roofline": roof, "cpu_baseline": cpu, "components": comps,
+        "roofline": roof, "cpu_baseline": cpu,
+        "graph_ms_per_step": r["graph_ms"],
+        "components": comps,
     }
     print(json.dumps(line), flush=True)
 
