@@ -712,6 +712,38 @@ def test_bsa_empty_rows_and_token_maps(ops):
     assert (got[128:256, 0] == 0).all()
 
 
+@pytest.mark.parametrize("order", ["growing", "shrinking"])
+def test_bsa_running_max_moves_every_block(ops, order):
+    """Key block j scaled by 2(j+1) (or in reverse): the largest score grows
+    by more than the kernel's 2^8 rescale threshold at every block, so the
+    running max and the O rescale run at each step ("growing"), or only at
+    the first ("shrinking"); both against the float64 oracle.  The softmax is
+    peaked here, so each output is a few rows of v: P is rounded to bf16
+    before the PV product, as the reference does (lcsa/triton_lcsa.py:55),
+    which moves a convex combination by at most 2 * 2^-9 * max|v|, and the
+    bf16 output adds 2^-9 * |o|; the bar is 2^-8 * (max|v| + 1)."""
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    H, D, NQ, NK = 2, 128, 2, 8
+    rng = np.random.default_rng(21)
+    q = rng.standard_normal((NQ * 128, H, D)).astype(np.float32)
+    k = rng.standard_normal((NK * 128, H, D)).astype(np.float32)
+    v = rng.standard_normal((NK * 128, H, D)).astype(np.float32)
+    f = 2.0 * np.arange(1, NK + 1)
+    if order == "shrinking":
+        f = f[::-1].copy()
+    k *= np.repeat(f, 128)[:, None, None].astype(np.float32)
+    q, k, v = O.bf16(q), O.bf16(k), O.bf16(v)
+    keep = np.ones((H, NQ, NK), bool)
+    keep[1, 1, ::2] = False  # a sparse row as well
+    ref = O.sparse_attention(q, k, v, keep)
+    out = torch.empty((NQ * 128, H, D), dtype=torch.bfloat16, device=DEV)
+    block_sparse_attention_strided(
+        dev_bf16(O.bf16_bits(q)), dev_bf16(O.bf16_bits(k)), dev_bf16(O.bf16_bits(v)),
+        torch.from_numpy(keep).to(DEV), None, heads=H, head_dim=D, q_strides=(H * D, D),
+        kv_strides=(H * D, D), out=out)
+    _attn_check(host_f(out), ref, tol=2.0 ** -8 * (float(np.abs(v).max()) + 1.0))
+
+
 def test_compat_bsa_func(ops):
     import block_sparse_attn
     rng = np.random.default_rng(10)
