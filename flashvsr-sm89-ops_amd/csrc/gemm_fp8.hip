@@ -284,10 +284,10 @@ FVSR_DEV void issue_pair(uint8_t LDS_AS* slot, i32x4_t ra, i32x4_t rb, int k0,
 #pragma unroll
   for (int t = 0; t < 8; ++t) {
     if (t < LA)
-      fvsr_buffer_load_lds(ra, (void LDS_AS*)(slot + (wave * LA + t) * 1024), 16, (int)o.a[t],
-                           k0, 0, 0);
+      fvsr_buffer_load_lds(ra, (void LDS_AS*)(slot + (wave * LA + t) * 1024), 16,
+                           __builtin_bit_cast(int, o.a[t]), k0, 0, 0);
     fvsr_buffer_load_lds(rb, (void LDS_AS*)(slot + Tile<MJ>::TM * 128 + (wave * 8 + t) * 1024),
-                         16, (int)o.b[t], k0, 0, 0);
+                         16, __builtin_bit_cast(int, o.b[t]), k0, 0, 0);
   }
 }
 
@@ -579,8 +579,11 @@ FVSR_DEV void fast_read(const uint16_t LDS_AS* stg, u32x4_t (&v)[4], int lane) {
   }
 }
 
+// Byte offsets into the output are unsigned 32-bit (the host admits outputs
+// below 4 GiB); the sum is formed in uint32_t and handed to the intrinsic's
+// int operand bit for bit.
 template <int EPI>
-FVSR_DEV void fast_store(const u32x4_t (&v)[4], float (&vmax)[4], i32x4_t rc, int voff,
+FVSR_DEV void fast_store(const u32x4_t (&v)[4], float (&vmax)[4], i32x4_t rc, uint32_t voff,
                          int64_t ldc, int ip, int j) {
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
@@ -588,7 +591,8 @@ FVSR_DEV void fast_store(const u32x4_t (&v)[4], float (&vmax)[4], i32x4_t rc, in
 #pragma unroll
       for (int w = 0; w < 4; ++w) vmax[s] = fmaxf(vmax[s], fmaxf(bf_lo(v[s][w]), bf_hi(v[s][w])));
     }
-    fvsr_buffer_store_b128(v[s], rc, voff + (int)((j * 32 + s * 8) * ldc * 2 + ip * 128), 0, 0);
+    const uint32_t off = voff + (uint32_t)((j * 32 + s * 8) * ldc * 2 + ip * 128);
+    fvsr_buffer_store_b128(v[s], rc, __builtin_bit_cast(int, off), 0, 0);
   }
 }
 
@@ -604,7 +608,7 @@ FVSR_DEV void epi_fast(const v16f (&acc)[4][MJ], uint16_t LDS_AS* stg, const uin
   // Store offset of row lane / 8, chunk lane % 8; each pass adds its row
   // block, row group and column half (all in the offset the range check
   // covers).
-  const int voff = (int)(((mw + (lane >> 3)) * e.ldc + nw + (lane & 7) * 8) * 2);
+  const uint32_t voff = (uint32_t)(((mw + (lane >> 3)) * e.ldc + nw + (lane & 7) * 8) * 2);
   float vmax[MJ][4];
 #pragma unroll
   for (int j = 0; j < MJ; ++j)

@@ -6,6 +6,17 @@ aireet/flashvsr-sm89-ops; every op runs hand-written HIP kernels from
 libfvsr.so through a C ABI (include/fvsr.h).  Importing the package installs
 the HIP-backed ``block_sparse_attn`` module (see compat_bsa), so import it
 before diffsynth, whose DiT imports block_sparse_attn at module load.
+
+What differs from the reference package at its public surface:
+- the tiling helpers (``plan_tiles``, ``render_tiled``, ``auto_tile_limits``,
+  ``tile_weight``) are not part of this build: they drive the pipeline over
+  spatial tiles and call none of these ops, so they stay with the reference;
+  ``from flashvsr_sm89_ops import render_tiled`` raises ImportError;
+- activations and weights must be bfloat16 (the dtype the FlashVSR DiT runs
+  in); the reference's kernels also accept fp16/fp32, these raise TypeError;
+- ``build_csr(keep)`` returns ``sel`` of width NK (``maxk = NK``, entries
+  past ``cnt`` unspecified) instead of trimming to the largest count, so no
+  host synchronisation is needed.
 """
 from .compat_bsa import active_backend, ensure_bsa_available
 

@@ -23,27 +23,75 @@ from . import _lib
 from .fp8_quant import FP8_MAX, quantize_fp8, quantize_weight_fp8  # noqa: F401
 
 
+def _check_gemm_args(x8, s, w8, w_scale, bias, out, epilogue, amax_part, res, gate):
+    """Operand checks of fp8_gemm: everything the kernel indexes must exist
+    at the size it assumes."""
+    _lib.require_dtype(x8, torch.float8_e4m3fn, "x8")
+    _lib.require_dtype(w8, torch.float8_e4m3fn, "weight")
+    if x8.dim() != 2 or w8.dim() != 2:
+        raise ValueError(f"fp8_gemm: x8 and weight must be 2-D, got {tuple(x8.shape)} and "
+                         f"{tuple(w8.shape)}")
+    M, K = x8.shape
+    N, K2 = w8.shape
+    if K != K2:
+        raise ValueError(f"fp8_gemm: K mismatch {K} vs {K2}")
+    if s.numel() not in (1, M) or w_scale.numel() not in (1, N):
+        raise ValueError("fp8_gemm: scale shapes must be per-tensor or per-row/column")
+    if bias is not None and (bias.dim() != 1 or bias.numel() != N):
+        raise ValueError(f"fp8_gemm: bias must be 1-D with N={N} elements, got "
+                         f"{tuple(bias.shape)}")
+    if epilogue not in (_lib.EPI_BIAS, _lib.EPI_ROWMAX, _lib.EPI_GATE_ADD):
+        raise ValueError(f"fp8_gemm: unknown epilogue {epilogue}")
+    if out is not None:
+        _lib.require_dtype(out, torch.bfloat16, "out")
+        if tuple(out.shape) != (M, N) or out.stride(1) != 1 or out.stride(0) < N:
+            raise ValueError(f"fp8_gemm: out must be [{M}, {N}] with unit column stride, got "
+                             f"shape {tuple(out.shape)} strides {out.stride()}")
+    ldc = out.stride(0) if out is not None else N
+    if epilogue == _lib.EPI_ROWMAX:
+        need = M * int(_lib.lib().fvsr_gemm_amax_parts(N))
+        if amax_part is None:
+            raise ValueError("fp8_gemm: the row-max epilogue needs amax_part")
+        _lib.require_dtype(amax_part, torch.float32, "amax_part")
+        if not amax_part.is_contiguous() or amax_part.numel() < need:
+            raise ValueError(f"fp8_gemm: amax_part needs {need} contiguous fp32 elements "
+                             f"(M * ceil(N/128)), got {amax_part.numel()}")
+    if epilogue == _lib.EPI_GATE_ADD:
+        if res is None or gate is None:
+            raise ValueError("fp8_gemm: the gate-add epilogue needs res and gate")
+        _lib.require_dtype(res, torch.bfloat16, "res")
+        _lib.require_dtype(gate, torch.bfloat16, "gate")
+        if tuple(res.shape) != (M, N) or res.stride(1) != 1 or res.stride(0) != ldc:
+            raise ValueError(f"fp8_gemm: res must be [{M}, {N}] with out's row stride {ldc}, "
+                             f"got shape {tuple(res.shape)} strides {res.stride()}")
+        if gate.numel() != N or not gate.is_contiguous():
+            raise ValueError(f"fp8_gemm: gate must hold N={N} contiguous elements, got "
+                             f"{tuple(gate.shape)}")
+
+
 def fp8_gemm(x8: torch.Tensor, s: torch.Tensor, w8: torch.Tensor, w_scale: torch.Tensor,
              bias: torch.Tensor | None = None, out: torch.Tensor | None = None,
              epilogue: int = _lib.EPI_BIAS, amax_part: torch.Tensor | None = None,
              res: torch.Tensor | None = None, gate: torch.Tensor | None = None) -> torch.Tensor:
     """bf16(x8 @ w8.T * s * w_scale + bias): x8 [M,K] e4m3, w8 [N,K] e4m3,
-    s [1]/[M]/[M,1] fp32, w_scale 0-dim/[1]/[N] fp32, bias [N] bf16 or None."""
-    _lib.require_gpu(x8, s, w8, w_scale, bias, out, res, gate)
-    _lib.require_dtype(x8, torch.float8_e4m3fn, "x8")
-    _lib.require_dtype(w8, torch.float8_e4m3fn, "weight")
+    s [1]/[M]/[M,1] fp32, w_scale 0-dim/[1]/[N] fp32, bias [N] bf16 or None.
+
+    ``out`` (optional) is [M, N] bf16 with unit column stride; epilogue
+    EPI_ROWMAX needs ``amax_part`` fp32 with M * ceil(N/128) contiguous
+    elements, EPI_GATE_ADD needs ``res`` [M, N] bf16 laid out like ``out``
+    (same row stride) and ``gate`` [N] bf16.  Every size is checked here,
+    before the launch, as torch._scaled_mm checks its operands (reference
+    fp8_linear.py:28-30); a mismatch raises ValueError / TypeError."""
+    _check_gemm_args(x8, s, w8, w_scale, bias, out, epilogue, amax_part, res, gate)
+    _lib.require_gpu(x8, s, w8, w_scale, bias, out, amax_part, res, gate)
     M, K = x8.shape
-    N, K2 = w8.shape
-    if K != K2:
-        raise ValueError(f"fp8_gemm: K mismatch {K} vs {K2}")
+    N = w8.shape[0]
     if x8.stride(1) != 1:
         x8 = x8.contiguous()
     if w8.stride(1) != 1:
         w8 = w8.contiguous()
     sa_mode = _lib.SCALE_ROW if s.numel() == M and M != 1 else _lib.SCALE_TENSOR
     sb_mode = _lib.SCALE_ROW if w_scale.numel() == N and N != 1 else _lib.SCALE_TENSOR
-    if s.numel() not in (1, M) or w_scale.numel() not in (1, N):
-        raise ValueError("fp8_gemm: scale shapes must be per-tensor or per-row/column")
     s = s.float().contiguous()
     w_scale = w_scale.float().contiguous()
     if bias is not None:
@@ -145,6 +193,9 @@ class FP8Linear(nn.Module):
         w_scale = w_scale.float()
         if w_scale.numel() not in (1, N):
             raise ValueError(f"from_quantized: {w_scale.numel()} scales for {N} output channels")
+        if bias is not None and (bias.dim() != 1 or bias.numel() != N):
+            raise ValueError(f"from_quantized: bias must be 1-D with {N} elements, got "
+                             f"{tuple(bias.shape)}")
         if w_scale.numel() == 1:
             w_scale = w_scale.reshape(())  # the reference keeps a 0-dim per-tensor scale
         m = cls(None, per_channel=w_scale.numel() == N and N != 1, per_token=per_token)
@@ -216,6 +267,12 @@ def convert_linears_fp8(model: nn.Module, parts=("ffn", "self", "cross"), per_ch
 FP8_WEIGHTS_FORMAT = "flashvsr-fp8-weights/2"
 
 
+class FP8WeightsFormatError(ValueError):
+    """A weight file written by an earlier version of save_fp8_weights (an
+    older ``flashvsr-fp8-weights/<n>`` format): its codes cannot be used
+    as they are, but quantising again and overwriting it is safe."""
+
+
 def save_fp8_weights(model: nn.Module, path: str) -> int:
     """Persist every FP8Linear of ``model`` (codes as uint8 bit patterns, fp32
     scales, bf16 biases, and in the metadata the fingerprint of the weights
@@ -247,7 +304,11 @@ def load_fp8_weights(path: str) -> StoredFP8Weights:
     from safetensors import safe_open
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = f.metadata() or {}
-        if meta.get("format") != FP8_WEIGHTS_FORMAT:
+        fmt = meta.get("format") or ""
+        if fmt != FP8_WEIGHTS_FORMAT:
+            if fmt.startswith(FP8_WEIGHTS_FORMAT.split("/")[0] + "/"):
+                raise FP8WeightsFormatError(f"{path}: {fmt} file, this version reads "
+                                            f"{FP8_WEIGHTS_FORMAT}; delete it to quantise again")
             raise ValueError(f"{path}: not a {FP8_WEIGHTS_FORMAT} file")
         out = StoredFP8Weights(fingerprints=json.loads(meta.get("fingerprints", "{}")))
         keys = set(f.keys())

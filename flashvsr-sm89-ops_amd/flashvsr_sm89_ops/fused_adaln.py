@@ -64,6 +64,9 @@ def fused_gate_add(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor):
     """x + gate * residual. x/residual [B, L, D] contiguous bf16; gate [B, 1, D]."""
     B, L, D = x.shape
     assert x.is_contiguous() and residual.is_contiguous() and gate.is_contiguous()
+    if residual.shape != x.shape:
+        raise ValueError(f"fused_gate_add: residual {tuple(residual.shape)} does not match x "
+                         f"{tuple(x.shape)}")
     _lib.require_gpu(x, gate, residual)
     _lib.require_dtype(residual, torch.bfloat16, "residual")
     _check_params(x, gate)

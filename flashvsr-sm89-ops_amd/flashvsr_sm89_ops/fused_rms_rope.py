@@ -67,12 +67,21 @@ def _table_for(freqs, L: int, head_dim: int, device) -> torch.Tensor:
     return t
 
 
+def _check_weights(D: int, *weights):
+    """RMSNorm weights must hold one element per channel of the D-wide rows
+    (the kernels read D of them)."""
+    for w in weights:
+        if w.numel() != D:
+            raise ValueError(f"RMSNorm weight has {w.numel()} elements, rows have D={D}")
+
+
 def fused_rms_rope(x: torch.Tensor, weight: torch.Tensor, freqs_cis, eps: float = 1e-6,
                    rope: bool = True, head_dim: int = 128):
     """x [B, L, D] bf16 -> RMSNorm(weight) -> [x RoPE] (fused_rms_rope.py:66-83)."""
+    B, L, D = x.shape
+    _check_weights(D, weight)
     _lib.require_gpu(x, weight)
     _lib.require_dtype(x, torch.bfloat16, "x")
-    B, L, D = x.shape
     x2 = x.contiguous()
     w = weight.to(torch.bfloat16).contiguous()
     out = torch.empty_like(x2)
@@ -91,10 +100,11 @@ def fused_rms_rope_qk(q: torch.Tensor, k: torch.Tensor, weight_q: torch.Tensor,
     q, k: [B, L, D] bf16 whose rows may be strided (e.g. column slices of a
     fused QKV output, last dim contiguous).  ``inplace`` writes the results
     over q and k."""
-    _lib.require_gpu(q, k, weight_q, weight_k)
     B, L, D = q.shape
     if k.shape != q.shape:
         raise ValueError("fused_rms_rope_qk: q and k shapes differ")
+    _check_weights(D, weight_q, weight_k)
+    _lib.require_gpu(q, k, weight_q, weight_k)
     if q.stride(-1) != 1 or k.stride(-1) != 1 or q.stride(1) != k.stride(1) or \
             (B > 1 and (q.stride(0) != L * q.stride(1) or k.stride(0) != L * k.stride(1))):
         q, k = q.contiguous(), k.contiguous()
@@ -126,7 +136,6 @@ def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     tensors or column slices of a fused qkv); q is rotated in place and returned;
     row r of k and v goes to row ``kv_rows[r]`` of ``out_k`` / ``out_v``
     ([rows, D] bf16, contiguous)."""
-    _lib.require_gpu(q, k, v, weight_q, weight_k, out_k, out_v, kv_rows)
     for t, n in ((q, "q"), (k, "k"), (v, "v"), (out_k, "out_k"), (out_v, "out_v")):
         _lib.require_dtype(t, torch.bfloat16, n)
     _lib.require_dtype(kv_rows, torch.int32, "kv_rows")
@@ -143,6 +152,8 @@ def fused_rms_rope_qkv_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         raise ValueError("fused_rms_rope_qkv_rows: out_k/out_v must be contiguous [rows, D]")
     if kv_rows.numel() != B * L or not kv_rows.is_contiguous():
         raise ValueError("fused_rms_rope_qkv_rows: kv_rows must hold B*L entries")
+    _check_weights(D, weight_q, weight_k)
+    _lib.require_gpu(q, k, v, weight_q, weight_k, out_k, out_v, kv_rows)
     wq = weight_q.to(torch.bfloat16).contiguous()
     wk = weight_k.to(torch.bfloat16).contiguous()
     cs = _table_for(freqs_cis, L, head_dim, q.device)

@@ -43,7 +43,8 @@ from .compat_bsa import active_backend, ensure_bsa_available
 from .cross_attn import cross_attention, unit_gate
 from .cross_attn import supported as cross_supported
 from .fp8_ffn import FP8FFN, convert_ffn_fp8, gemm_gelu_quant_fp8
-from .fp8_linear import FP8Linear, convert_linears_fp8, fp8_gemm, load_fp8_weights, save_fp8_weights
+from .fp8_linear import (FP8Linear, FP8WeightsFormatError, convert_linears_fp8, fp8_gemm,
+                         load_fp8_weights, save_fp8_weights)
 from .fp8_quant import quantize_fp8
 from .fused_adaln import (fused_gate_add, fused_gate_add_layer_norm,
                           fused_gate_add_ln_modulate_quant, fused_ln_modulate,
@@ -413,6 +414,13 @@ def _gated_residual_norm3(blk, x, gate, attn_out, gate_add):
     return x, normed
 
 
+def _per_token_ffn(ffn) -> bool:
+    """True for an FP8FFN whose two linears both quantise activations per
+    token: the only FFN the per-token codes dataflow may feed directly."""
+    return (isinstance(ffn, FP8FFN) and getattr(ffn.lin0, "per_token", False)
+            and getattr(ffn.lin2, "per_token", False))
+
+
 def _make_dit_block_forward(dit, stock):
     def forward(self, x, context, t_mod, freqs, f, h, w, local_num=None, topk=None,
                 train_img=False, block_id=None, kv_len=None, is_full_block=False,
@@ -448,9 +456,11 @@ def _make_dit_block_forward(dit, stock):
         yc = self.cross_attn(normed, context, is_stream=is_stream)
 
         # 3) FFN on the modulated LayerNorm of x + yc, gated residual
-        if codes and isinstance(self.ffn, FP8FFN) and yc.shape == x.shape and yc.is_contiguous():
+        if codes and _per_token_ffn(self.ffn) and yc.shape == x.shape and yc.is_contiguous():
             # x + yc (a unit gate) and the FFN's AdaLN in one pass; its
-            # per-token codes go straight into the FFN GEMMs
+            # per-token codes go straight into the FFN GEMMs (an FFN
+            # converted with per-tensor activation scales keeps its own
+            # forward, so its quantisation never changes)
             B, L, D = x.shape
             x, h8, hs = fused_gate_add_ln_modulate_quant(
                 x, unit_gate(D, x.device), yc, m.scale_mlp, m.shift_mlp, eps=_eps(self.norm2))
@@ -535,8 +545,12 @@ def _setup_fp8(model, parts, per_row: bool, weights_file) -> dict:
         return done
     stored = None
     if weights_file and os.path.exists(weights_file):
-        stored = load_fp8_weights(weights_file)
-        done["fp8_weights"] = "loaded"
+        try:
+            stored = load_fp8_weights(weights_file)
+            done["fp8_weights"] = "loaded"
+        except FP8WeightsFormatError as e:
+            # a file from an earlier version: quantise again and overwrite it
+            warnings.warn(f"{e}; quantising again and rewriting it", stacklevel=3)
     done["fp8_linears"] = convert_linears_fp8(model, parts=parts, per_channel=per_row,
                                               per_token=per_row, stored=stored)
     if weights_file and stored is None and done["fp8_linears"]:

@@ -16,7 +16,10 @@
  *    the hipStream_t passed as `stream` (NULL = the default stream).
  *  - Return value: FVSR_OK (0) or a negative fvsr_status.  Argument checks
  *    run on the host before anything is enqueued.
- *  - Reentrant: no mutable global state.
+ *  - Reentrant: no mutable global state, with one exception:
+ *    fvsr_quant_fp8_noalloc (below) keeps its scratch in one device array per
+ *    GPU plus a host table of those arrays' addresses, so calls of it that
+ *    overlap on one GPU race; every other entry point is reentrant.
  *
  * Each declaration names the reference interface (aireet/flashvsr-sm89-ops,
  * file:line) whose work it carries.

@@ -252,13 +252,14 @@ def test_enable_dit_block_vs_oracle(monkeypatch, row, draft, dim, heads, ffn):
         assert np.array_equal(rk.reshape(-1, dim), host_f(ck).reshape(-1, dim))
         assert np.array_equal(rv.reshape(-1, dim), host_f(cv).reshape(-1, dim))
         dev_cache = (host_f(ck), host_f(cv))
-        # 3. per token: the whole block against the oracle's own chain
-        if row:
-            ref, rk2, rv2 = O.dit_block(host_f(x)[0], mod, params, (f, h, w), keep, cs[..., 0],
-                                        cs[..., 1], heads, eps, cross=cross, per_token=True,
-                                        cache=ocache, kv_len=kv_len, return_cache=True)
-            frac, mx = _frac_beyond(host_f(y)[0], ref)
-            print(f"  step {step}: chain {frac:.2e} beyond 2e-2 (max {mx:.3g})", flush=True)
-            assert frac <= 5e-3, f"step {step}: chain {frac:.2e} beyond 2e-2, max {mx:.3g}"
-            ocache = (rk2, rv2)
+        # 3. the whole block against the oracle's own chain from the input,
+        # per token and per tensor (the reference's default), at the chain bar:
+        # at most 0.1% of elements beyond rtol/atol 2e-2
+        ref, rk2, rv2 = O.dit_block(host_f(x)[0], mod, params, (f, h, w), keep, cs[..., 0],
+                                    cs[..., 1], heads, eps, cross=cross, per_token=row,
+                                    cache=ocache, kv_len=kv_len, return_cache=True)
+        frac, mx = _frac_beyond(host_f(y)[0], ref)
+        print(f"  step {step}: chain {frac:.2e} beyond 2e-2 (max {mx:.3g})", flush=True)
+        assert frac <= 1e-3, f"step {step}: chain {frac:.2e} beyond 2e-2, max {mx:.3g}"
+        ocache = (rk2, rv2)
     assert dev_cache[0].shape[0] == 2 * (h // 8) * (w // 8)

@@ -703,3 +703,155 @@ def test_convert_ffn_fp8_swap_and_assertion():
         assert isinstance(up, FP8Linear) and isinstance(down, FP8Linear)
     assert isinstance(model.head, torch.nn.Sequential)
     assert convert_ffn_fp8(model) == 0
+
+
+def _gpu_only(fn, *a, **k):
+    """A call whose arguments pass every host-side check reaches the GPU
+    check, which rejects CPU tensors."""
+    with pytest.raises(RuntimeError, match="GPU only"):
+        fn(*a, **k)
+
+
+def test_fp8_gemm_size_checks():
+    """fp8_gemm rejects, before any launch, every operand whose size the
+    kernel would trust: bias length, out's shape / dtype / column stride,
+    the row-max partials' length and the gate-add residual and gate (the
+    checks torch._scaled_mm makes behind reference fp8_linear.py:28-30)."""
+    from flashvsr_sm89_ops import _lib
+    from flashvsr_sm89_ops.fp8_linear import fp8_gemm
+    M, N, K = 5, 300, 64
+    e4 = torch.float8_e4m3fn
+    x8, w8 = torch.zeros(M, K, dtype=e4), torch.zeros(N, K, dtype=e4)
+    s, ws = torch.ones(M), torch.ones(N)
+    bf = torch.bfloat16
+    _gpu_only(fp8_gemm, x8, s, w8, ws, torch.zeros(N, dtype=bf))
+    with pytest.raises(ValueError, match="bias"):
+        fp8_gemm(x8, s, w8, ws, torch.zeros(N - 1, dtype=bf))
+    with pytest.raises(ValueError, match="bias"):
+        fp8_gemm(x8, s, w8, ws, torch.zeros(1, N, dtype=bf))
+    with pytest.raises(ValueError, match="K mismatch"):
+        fp8_gemm(x8, s, torch.zeros(N, K + 16, dtype=e4), ws)
+    with pytest.raises(ValueError, match="scale"):
+        fp8_gemm(x8, torch.ones(M + 1), w8, ws)
+    # out: shape, dtype, unit column stride; a wider row stride is fine
+    _gpu_only(fp8_gemm, x8, s, w8, ws, out=torch.empty(M, N + 8, dtype=bf)[:, :N])
+    with pytest.raises(ValueError, match="out must be"):
+        fp8_gemm(x8, s, w8, ws, out=torch.empty(M, N - 1, dtype=bf))
+    with pytest.raises(ValueError, match="out must be"):
+        fp8_gemm(x8, s, w8, ws, out=torch.empty(N, M, dtype=bf).t())
+    with pytest.raises(TypeError, match="out"):
+        fp8_gemm(x8, s, w8, ws, out=torch.empty(M, N, dtype=torch.float16))
+    with pytest.raises(ValueError, match="epilogue"):
+        fp8_gemm(x8, s, w8, ws, epilogue=7)
+    # row maxima: M * ceil(N / 128) fp32
+    parts = (N + 127) // 128
+    _gpu_only(fp8_gemm, x8, s, w8, ws, epilogue=_lib.EPI_ROWMAX,
+              amax_part=torch.empty(M, parts))
+    with pytest.raises(ValueError, match="amax_part"):
+        fp8_gemm(x8, s, w8, ws, epilogue=_lib.EPI_ROWMAX)
+    with pytest.raises(ValueError, match="amax_part"):
+        fp8_gemm(x8, s, w8, ws, epilogue=_lib.EPI_ROWMAX, amax_part=torch.empty(M * parts - 1))
+    # gate-add: res [M, N] with out's row stride, gate [N]
+    res, gate = torch.zeros(M, N, dtype=bf), torch.zeros(N, dtype=bf)
+    _gpu_only(fp8_gemm, x8, s, w8, ws, epilogue=_lib.EPI_GATE_ADD, res=res, gate=gate)
+    with pytest.raises(ValueError, match="gate-add epilogue needs"):
+        fp8_gemm(x8, s, w8, ws, epilogue=_lib.EPI_GATE_ADD, res=res)
+    with pytest.raises(ValueError, match="res must be"):
+        fp8_gemm(x8, s, w8, ws, epilogue=_lib.EPI_GATE_ADD, res=res[:-1], gate=gate)
+    with pytest.raises(ValueError, match="res must be"):   # row stride differs from out's
+        fp8_gemm(x8, s, w8, ws, out=torch.empty(M, N + 8, dtype=bf)[:, :N],
+                 epilogue=_lib.EPI_GATE_ADD, res=res, gate=gate)
+    with pytest.raises(ValueError, match="gate must"):
+        fp8_gemm(x8, s, w8, ws, epilogue=_lib.EPI_GATE_ADD, res=res, gate=gate[:-1])
+
+
+def test_row_op_size_checks():
+    """fused_gate_add checks the residual against x; the RMSNorm(+RoPE)
+    entry points check the weight length against D;
+    FP8Linear.from_quantized checks the bias length."""
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    from flashvsr_sm89_ops.fused_adaln import fused_gate_add
+    from flashvsr_sm89_ops.fused_rms_rope import (fused_rms_rope, fused_rms_rope_qk,
+                                                  fused_rms_rope_qkv_rows)
+    bf = torch.bfloat16
+    B, L, D = 1, 6, 256
+    x = torch.zeros(B, L, D, dtype=bf)
+    gate = torch.zeros(B, 1, D, dtype=bf)
+    _gpu_only(fused_gate_add, x, gate, torch.zeros_like(x))
+    with pytest.raises(ValueError, match="residual"):
+        fused_gate_add(x, gate, torch.zeros(B, L - 1, D, dtype=bf))
+    w = torch.ones(D, dtype=bf)
+    _gpu_only(fused_rms_rope, x, w, None, rope=False)
+    with pytest.raises(ValueError, match="RMSNorm weight"):
+        fused_rms_rope(x, torch.ones(D - 2, dtype=bf), None, rope=False)
+    _gpu_only(fused_rms_rope_qk, x, x, w, w, None)
+    with pytest.raises(ValueError, match="RMSNorm weight"):
+        fused_rms_rope_qk(x, x, w, torch.ones(D + 2, dtype=bf), None)
+    kv = torch.zeros(L, D, dtype=bf)
+    rows = torch.arange(L, dtype=torch.int32)
+    _gpu_only(fused_rms_rope_qkv_rows, x, x, x, w, w, None, kv, kv.clone(), rows)
+    with pytest.raises(ValueError, match="RMSNorm weight"):
+        fused_rms_rope_qkv_rows(x, x, x, torch.ones(1, dtype=bf), w, None, kv, kv.clone(), rows)
+    codes = torch.zeros(8, 16, dtype=torch.float8_e4m3fn)
+    FP8Linear.from_quantized(codes, torch.ones(8), torch.zeros(8, dtype=bf))
+    with pytest.raises(ValueError, match="bias"):
+        FP8Linear.from_quantized(codes, torch.ones(8), torch.zeros(7, dtype=bf))
+
+
+def test_per_token_ffn_guard():
+    """The DiT block feeds per-token codes straight into the FFN GEMMs only
+    when both FFN linears quantise activations per token; an FFN converted
+    with per-tensor activation scales keeps FP8FFN.forward."""
+    from flashvsr_sm89_ops.fp8_ffn import FP8FFN
+    from flashvsr_sm89_ops.fp8_linear import FP8Linear
+    from flashvsr_sm89_ops.integrate import _per_token_ffn
+
+    def lin(n, k, per_token):
+        return FP8Linear.from_quantized(torch.zeros(n, k, dtype=torch.float8_e4m3fn),
+                                        torch.ones(n), per_token=per_token)
+    assert _per_token_ffn(FP8FFN(lin(32, 16, True), lin(16, 32, True)))
+    assert not _per_token_ffn(FP8FFN(lin(32, 16, False), lin(16, 32, False)))
+    assert not _per_token_ffn(FP8FFN(lin(32, 16, True), lin(16, 32, False)))
+    assert not _per_token_ffn(torch.nn.Sequential())
+
+
+def test_enable_rewrites_old_format_fp8_weights(tmp_path, monkeypatch):
+    """A weight file of an earlier format version is not an error for
+    enable(): it warns, quantises again and overwrites the file with the
+    current format; a file that is not an FP8 weight file at all is still
+    refused (nothing of the user's is overwritten)."""
+    import flashvsr_sm89_ops as f
+    from safetensors import safe_open
+    from safetensors.torch import save_file
+    from flashvsr_sm89_ops.fp8_linear import FP8_WEIGHTS_FORMAT, FP8WeightsFormatError, \
+        load_fp8_weights
+    path = str(tmp_path / "w.safetensors")
+    save_file({"blocks.0.self_attn.q.weight": torch.zeros(2, 2, dtype=torch.uint8)}, path,
+              metadata={"format": "flashvsr-fp8-weights/1"})
+    with pytest.raises(FP8WeightsFormatError, match="delete it"):
+        load_fp8_weights(path)
+    # quantising needs the GPU: on the CPU the conversion takes stand-in codes
+    import flashvsr_sm89_ops.integrate as integ
+    real = integ.convert_linears_fp8
+
+    def convert(model, parts, per_channel, per_token, stored):
+        assert stored is None                         # the old file was not used
+        return real(model, parts=parts, per_channel=per_channel, per_token=per_token,
+                    stored=_stored_for(model, per_channel))
+    monkeypatch.setattr(integ, "convert_linears_fp8", convert)
+    pipe = FakePipe()
+    pipe.model = _dit_like(seed=4)
+    monkeypatch.setenv("FS89_FP8", "self")
+    monkeypatch.setenv("FS89_FP8_WEIGHTS", path)
+    with pytest.warns(UserWarning, match="quantising again"):
+        applied = f.enable(pipe, dit_module=make_fake_dit(), verbose=False)
+    assert applied["fp8_weights"] == "saved" and applied["fp8_linears"] == 8
+    with safe_open(path, framework="pt") as fh:
+        assert fh.metadata()["format"] == FP8_WEIGHTS_FORMAT
+    other = str(tmp_path / "other.safetensors")
+    save_file({"x": torch.zeros(2)}, other)
+    pipe2 = FakePipe()
+    pipe2.model = _dit_like(seed=4)
+    monkeypatch.setenv("FS89_FP8_WEIGHTS", other)
+    with pytest.raises(ValueError, match="not a"):
+        f.enable(pipe2, dit_module=make_fake_dit(), verbose=False)

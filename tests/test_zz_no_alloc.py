@@ -2,7 +2,7 @@
 scratch) against fvsr_quant_fp8 (caller workspace), both through the C ABI:
 codes and scales bit-identical, on two calls in a row (the second with a
 smaller input, so stale partial maxima of the first would show), per tensor
-with and without GELU, and per row."""
+with and without GELU, and per row; and captured in a HIP graph, replayed."""
 import numpy as np
 import pytest
 import torch
@@ -32,6 +32,45 @@ def _both(L, x, mode, gelu):
         out.append((q, s))
     torch.cuda.synchronize()
     return out
+
+
+def test_noalloc_in_graph_capture():
+    """Captured in a HIP graph (torch.cuda.graph) and replayed: per tensor
+    with and without GELU, and per row, each replay bit-identical to the
+    workspace entry run eagerly on the same input, with eager work and a new
+    input between replays.  This test comes first in the file so that, in a
+    fresh process, the captured call is also the one that first resolves the
+    library's device scratch address (no other test calls the entry point
+    before it)."""
+    from flashvsr_sm89_ops import _lib
+    L = _lib.lib()
+    g = torch.Generator().manual_seed(77)
+    M, K = 3000, 1536
+    inputs = [(torch.randn(M, K, generator=g) * sc).to(torch.bfloat16) for sc in (4.0, 0.25, 9.0)]
+    x = inputs[0].to(DEV)
+    cases = [(0, 0), (0, 1), (1, 0)]
+    outs = [(torch.empty((M, K), dtype=torch.uint8, device=DEV),
+             torch.empty((M if mode else 1,), dtype=torch.float32, device=DEV))
+            for mode, _ in cases]
+    graph = torch.cuda.CUDAGraph()
+    rcs = []
+    with torch.cuda.graph(graph):
+        st = torch.cuda.current_stream().cuda_stream
+        for (mode, gelu), (q, s) in zip(cases, outs):
+            rcs.append(L.fvsr_quant_fp8_noalloc(x.data_ptr(), M, K, K, mode, gelu,
+                                                q.data_ptr(), s.data_ptr(), st))
+    assert rcs == [_lib.FVSR_OK] * len(cases), rcs
+    for rep, host in enumerate(inputs + inputs[:1]):
+        x.copy_(host.to(DEV))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [(q.clone(), s.clone()) for q, s in outs]
+        _ = (x.float() * 2).sum()          # eager work between replays
+        for (mode, gelu), (q, s) in zip(cases, got):
+            (q0, s0), _unused = _both(L, x, mode, gelu)
+            assert torch.equal(q0, q), f"replay {rep}: codes differ (mode {mode}, gelu {gelu})"
+            assert torch.equal(s0, s), f"replay {rep}: scales differ (mode {mode}, gelu {gelu})"
 
 
 @pytest.mark.parametrize("mode,gelu", [(0, 0), (0, 1), (1, 0), (1, 1)])
