@@ -849,24 +849,83 @@ def summarize_mfma(csv_path, simds=1024, xcds=8):
 
 
 def blaslt_same_box(torch):
-    """torch._scaled_mm (hipBLASLt) at the BASELINE GEMM shapes on this GPU,
-    per-tensor and row-wise scales, for comparison with fvsr_fp8_gemm."""
+    """torch._scaled_mm (hipBLASLt) against fvsr_fp8_gemm on the same operands
+    the bench's components feed the GEMMs: per-token e4m3 codes of
+    LayerNorm-modulated rows (C1: of N(0,1) rows) for qkv, o, ffn0 and C1,
+    GELU-requantised codes of ffn0's output for ffn2, per-channel weight codes
+    of N(0, 0.02) weights, row-wise scales and a bias.  Input sets rotate past
+    the 256 MB MALL and the two libraries are timed alternately, twice each
+    (the better of the two runs is reported), on the same stream."""
+    from flashvsr_sm89_ops import fp8_gemm, fused_gelu_quant_fp8, fused_ln_modulate_quant, \
+        quantize_fp8, quantize_weight_fp8
     dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def randn(*s, std=1.0):
+        return (torch.randn(*s, generator=g, device=dev) * std).to(torch.bfloat16)
+
+    mod = (0.1 * torch.randn(1, 6, DIM, generator=g, device=dev)).to(torch.bfloat16)
+    sh, sc = mod[:, 3:4].contiguous(), mod[:, 4:5].contiguous()
+
+    def ln_codes(M, K, n):
+        return [fused_ln_modulate_quant(randn(1, M, K), sc[..., :K].contiguous(),
+                                        sh[..., :K].contiguous()) for _ in range(n)]
+
     rows = []
-    for (M, N, K) in [(4224, 1536, 1536), (16896, 4608, 1536), (16896, 1536, 1536),
-                      (16896, 8960, 1536), (16896, 1536, 8960), (8192, 8192, 8192)]:
-        a = torch.randint(-100, 100, (M, K), device=dev).to(torch.float8_e4m3fn)
-        b = torch.randint(-100, 100, (N, K), device=dev).to(torch.float8_e4m3fn)
-        for mode in ("tensor", "row"):
-            if mode == "tensor":
-                sa, sb = torch.ones((), device=dev), torch.ones((), device=dev)
-            else:
-                sa, sb = torch.ones((M, 1), device=dev), torch.ones((1, N), device=dev)
-            t = timeit(torch, lambda i: torch._scaled_mm(a, b.t(), scale_a=sa, scale_b=sb,
-                                                         out_dtype=torch.bfloat16), 1, iters=20)
-            rows.append({"M": M, "N": N, "K": K, "scales": mode, "us": t * 1e3,
-                         "TFLOPs": 2 * M * N * K / (t * 1e-3) / 1e12})
-        del a, b
+    shapes = [("C1", 4224, 1536, 1536), ("qkv", L, 3 * DIM, DIM), ("o", L, DIM, DIM),
+              ("ffn0", L, FFN, DIM), ("ffn2", L, DIM, FFN)]
+    w1 = None
+    for name, M, N, K in shapes:
+        w8, ws = quantize_weight_fp8(randn(N, K, std=0.02), per_channel=True)
+        bias = randn(N, std=0.02)
+        n = n_sets_for(M * K + M * N * 2)
+        if name == "C1":
+            xs = [quantize_fp8(randn(M, K), per_token=True) for _ in range(n)]
+        elif name == "ffn2":
+            src = ln_codes(M, DIM, 2)
+            xs = []
+            for i in range(n):
+                h = fp8_gemm(src[i % 2][0], src[i % 2][1], w1[0], w1[1], w1[2])
+                xs.append(fused_gelu_quant_fp8(h, per_token=True))
+                del h
+        else:
+            xs = ln_codes(M, K, n)
+        if name == "ffn0":
+            w1 = (w8, ws, bias)
+        outs = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        sb_row = ws.reshape(1, N).contiguous()
+        sa_rows = [x[1].reshape(M, 1).contiguous() for x in xs]
+
+        def ours(i):
+            fp8_gemm(xs[i][0], xs[i][1], w8, ws, bias, out=outs[0])
+
+        use_bias = True
+
+        def theirs(i):
+            return torch._scaled_mm(xs[i][0], w8.t(), scale_a=sa_rows[i], scale_b=sb_row,
+                                    bias=bias if use_bias else None, out_dtype=torch.bfloat16)
+        try:
+            theirs(0)
+        except RuntimeError:
+            use_bias = False       # row-wise scales with a bias unsupported: time without
+        t_ours, t_theirs = [], []
+        for _ in range(2):
+            t_ours.append(timeit(torch, ours, n, iters=20))
+            t_theirs.append(timeit(torch, theirs, n, iters=20))
+        ours(0)
+        ref = theirs(0)
+        torch.cuda.synchronize()
+        diff = (outs[0].float() - ref.float()).abs()
+        flop = 2 * M * N * K
+        rows.append({"gemm": name, "M": M, "N": N, "K": K, "scales": "row x channel",
+                     "bias_in_blaslt": use_bias,
+                     "fvsr_us": min(t_ours) * 1e3, "blaslt_us": min(t_theirs) * 1e3,
+                     "fvsr_TFLOPs": flop / (min(t_ours) * 1e-3) / 1e12,
+                     "blaslt_TFLOPs": flop / (min(t_theirs) * 1e-3) / 1e12,
+                     "max_abs_diff": float(diff.max()),
+                     "frac_bitwise_equal": float((diff == 0).float().mean()) if use_bias else None,
+                     "input_sets": n})
+        del xs, outs, ref
     return rows
 
 
