@@ -60,6 +60,10 @@ _SIGS = {
                                _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P], _I),
     "fvsr_bsa_fwd": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64,
                       _I64, _I64, _I64, _F, _P, _P, _P], _I),
+    "fvsr_attn_dense": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                         _I64, _F, _P], _I),
+    "fvsr_bsa_fwd_window": ([_P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _P, _I64,
+                             _I64, _I64, _I64, _I64, _F, _I64, _I64, _I64, _I, _P], _I),
 }
 
 _lib = None

@@ -91,12 +91,14 @@ def _modulation(wts: DiTBlockWeights, t_mod: torch.Tensor):
 
 
 def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor, cs: torch.Tensor,
-                      index, tok_map: torch.Tensor, heads: int = 12, eps: float = 1e-6,
+                      index, tok_map, heads: int = 12, eps: float = 1e-6,
                       hook=None, x8s=None, next_wts: DiTBlockWeights | None = None,
                       mods=None, next_mods=None):
     """x [1, L, dim] bf16 (raster order) -> [1, L, dim].  ``index`` is the
     device block index (sel, cnt, maxk) of the attention mask; ``tok_map``
-    is window_token_map(f, h, w); ``cs`` the (cos, sin) table [L, 64, 2].
+    is the latent grid ``(f, h, w)`` whose (2, 8, 8) windows are the attention
+    blocks (the kernel computes the window order), or window_token_map(f, h,
+    w) itself (read as a gathered map); ``cs`` the (cos, sin) table [L, 64, 2].
 
     Each gated residual (integrate.py:163-182) is fused with the AdaLN that
     follows it: the self-attention's with the FFN's, the FFN's with the next
@@ -128,7 +130,9 @@ def dit_block_forward(x: torch.Tensor, wts: DiTBlockWeights, t_mod: torch.Tensor
     block_sparse_attention_strided(
         qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:], None, 1.0 / math.sqrt(hd), heads=heads,
         head_dim=hd, q_strides=(3 * D, hd), kv_strides=(3 * D, hd), out=attn,
-        o_strides=(D, hd), q_map=tok_map, kv_map=tok_map, index=index)
+        o_strides=(D, hd), index=index,
+        **({"q_map": tok_map, "kv_map": tok_map} if torch.is_tensor(tok_map)
+           else {"window": (*tok_map, True)}))
 
     mark("quant_attn")
     a8, as_ = quantize_fp8(attn, per_token=True)

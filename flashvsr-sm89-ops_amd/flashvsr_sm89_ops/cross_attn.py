@@ -4,9 +4,9 @@ Reference path (flashvsr_sm89_ops/integrate.py:132-143,171):
 ``x + cross_attn(norm3(x), context)`` with ``norm3`` an affine LayerNorm, an
 FP8 q projection, RMSNorm of q (no RoPE), dense attention of the 16896 video
 tokens over the prompt K/V cached by ``init_cross_kv``, and an FP8 o
-projection.  Here the dense attention runs on the block-sparse attention
-kernel with every 128-key block kept (an all-kept block index, built once per
-shape on the device), the LayerNorm emits the q projection's per-token e4m3
+projection.  Here the dense attention runs on the attention kernel's dense
+mode (fvsr_attn_dense: every 128-key block, no block index, two query blocks
+per workgroup over one K/V stream), the LayerNorm emits the q projection's per-token e4m3
 codes in the same pass, and the residual add is a gate-add
 add with a unit gate (bf16(x + bf16(1 * y)) = bf16(x + y)), which inside a DiT
 block is fused with the AdaLN that follows it.
@@ -21,24 +21,10 @@ from .fp8_linear import fp8_gemm
 from .fp8_quant import quantize_fp8
 from .fused_adaln import fused_gate_add, layer_norm_quant
 from .fused_rms_rope import fused_rms_rope
-from .lcsa.hip_lcsa import block_sparse_attention_strided
+from .lcsa.hip_lcsa import dense_attention_strided
 
 BLOCK = 128
-_INDEX = {}
 _ONES = {}
-
-
-def dense_index(heads: int, nq: int, nk: int, device) -> tuple:
-    """All-kept block index (sel, cnt, maxk) for heads x nq query blocks over
-    nk key blocks, cached per shape and device."""
-    key = (heads, nq, nk, str(device))
-    idx = _INDEX.get(key)
-    if idx is None:
-        sel = torch.arange(nk, dtype=torch.int32, device=device).expand(heads, nq, nk).contiguous()
-        cnt = torch.full((heads, nq), nk, dtype=torch.int32, device=device)
-        idx = (sel, cnt, nk)
-        _INDEX[key] = idx
-    return idx
 
 
 def supported(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads: int) -> bool:
@@ -76,11 +62,10 @@ def cross_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, num_heads
         k2 = k2.contiguous()
     if out is None:
         out = torch.empty((1, Lq, HD), dtype=torch.bfloat16, device=q.device)
-    idx = dense_index(num_heads, Lq // BLOCK, Lk // BLOCK, q.device)
-    block_sparse_attention_strided(
-        q2, k2, v2, None, sm_scale if sm_scale is not None else 1.0 / math.sqrt(hd),
+    dense_attention_strided(
+        q2, k2, v2, sm_scale if sm_scale is not None else 1.0 / math.sqrt(hd),
         heads=num_heads, head_dim=hd, q_strides=(q2.stride(0), hd),
-        kv_strides=(k2.stride(0), hd), out=out[0], o_strides=(HD, hd), index=idx)
+        kv_strides=(k2.stride(0), hd), out=out[0], o_strides=(HD, hd))
     return out
 
 

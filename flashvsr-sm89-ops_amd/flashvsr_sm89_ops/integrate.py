@@ -121,9 +121,10 @@ _MAPS: dict = {}
 
 
 def _window_maps(f, h, w, n_cache_rows, device):
-    """(tok, kv_rows, kv_map) for one geometry: tok[i] = raster token at window
-    position i; kv_rows[t] = row of raster token t in the K/V buffer (after the
-    cached rows); kv_map = identity over the whole K/V buffer."""
+    """(tok, kv_rows) for one geometry: tok[i] = raster token at window
+    position i (the draft mask reads q through it); kv_rows[t] = row of raster
+    token t in the K/V buffer (after the cached rows).  The attention itself
+    computes the window order (fvsr_bsa_fwd_window)."""
     key = (f, h, w, n_cache_rows, str(device))
     hit = _MAPS.get(key)
     if hit is not None:
@@ -131,8 +132,7 @@ def _window_maps(f, h, w, n_cache_rows, device):
     tok = window_token_map(f, h, w, device=device)
     pos = torch.empty_like(tok)
     pos[tok.long()] = torch.arange(tok.numel(), dtype=torch.int32, device=device)
-    val = (tok, (pos + n_cache_rows).contiguous(),
-           torch.arange(n_cache_rows + tok.numel(), dtype=torch.int32, device=device))
+    val = (tok, (pos + n_cache_rows).contiguous())
     while len(_MAPS) >= 32:          # a handful of geometries per run
         _MAPS.pop(next(iter(_MAPS)))
     _MAPS[key] = val
@@ -266,7 +266,7 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
     kbuf, vbuf = _kv_buffers(self, pre_cache_k, pre_cache_v, cache_rows, L, D, q, is_stream)
     if _eps(self.norm_k) != _eps(self.norm_q):
         raise NotImplementedError("q and k RMSNorm eps differ")
-    tok, kv_rows, kv_map = _window_maps(f, h, w, cache_rows, q.device)
+    tok, kv_rows = _window_maps(f, h, w, cache_rows, q.device)
     fused_rms_rope_qkv_rows(q, k, v, _inner(self.norm_q).weight, _inner(self.norm_k).weight,
                             freqs, kbuf, vbuf, kv_rows, eps=_eps(self.norm_q),
                             head_dim=self.head_dim)
@@ -287,7 +287,7 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
     block_sparse_attention_strided(
         q2, kbuf, vbuf, None, None, heads=self.num_heads, head_dim=hd,
         q_strides=(q2.stride(0), hd), kv_strides=(D, hd), out=out, o_strides=(D, hd),
-        q_map=tok, kv_map=kv_map, index=index)
+        window=(f, h, w, False), index=index)
     cache_k, cache_v = _trim_cache(k_w, v_w, windows_per_step, kv_len)
     y = self.o(out.view(B, L, D))
     return (y, cache_k, cache_v) if is_stream else y

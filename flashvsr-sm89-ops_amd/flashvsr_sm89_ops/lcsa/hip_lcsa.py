@@ -68,26 +68,41 @@ def _check_index(sel, cnt, maxk, H, NQ):
 
 def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, head_dim: int,
                                    q_strides, kv_strides, out=None, o_strides=None,
-                                   q_map=None, kv_map=None, index=None):
+                                   q_map=None, kv_map=None, index=None, window=None):
     """General entry: q/k/v/out bf16 with (token stride, head stride) in
     elements; keep [H, NQ, NK] (or a prebuilt ``index=(sel, cnt, maxk)``).
 
+    ``window=(frames, height, width, kv_raster)`` (instead of maps): q/out rows
+    are raster tokens of that latent grid read in the (2, 8, 8) window order of
+    WindowPartition3D (integrate.py:70-94), computed in the kernel
+    (fvsr_bsa_fwd_window); kv_raster says k/v are raster tokens of the same
+    grid too, otherwise they are already in window order.
+
     Checked before the launch: the index covers H x NQ rows of maxk entries
     (contiguous int32); without maps, q/out hold NQ*128 tokens and k/v NK*128
-    at their strides; maps are int32 with at least NQ*128 / NK*128 entries.
+    at their strides; maps are int32 with at least NQ*128 / NK*128 entries;
+    a window grid covers exactly NQ*128 tokens.
     Not checked (a host sync would be needed): that map entries lie inside
     their tensors and that sel/cnt values lie inside [0, NK) / [0, maxk], as
     build_csr and the device draft mask produce them."""
-    _lib.require_gpu(q, k, v, out, q_map, kv_map)
     for t, n in ((q, "q"), (k, "k"), (v, "v")):
         _lib.require_dtype(t, torch.bfloat16, n)
     if index is None:
-        sel, cnt, maxk = build_csr(keep)
         H, NQ, NK = keep.shape
     else:
-        sel, cnt, maxk = index
-        H, NQ = cnt.shape
-        NK = maxk
+        H, NQ = index[1].shape
+        NK = index[2]
+    if window is not None:
+        if q_map is not None or kv_map is not None:
+            raise ValueError("give either token maps or a window grid, not both")
+        frames, height, width, kv_raster = window
+        if frames % 2 or height % 8 or width % 8 or frames * height * width != NQ * BLOCK:
+            raise ValueError(f"window grid {frames}x{height}x{width} is not NQ={NQ} windows "
+                             "of 2x8x8 tokens")
+        if kv_raster and NK != NQ:
+            raise ValueError("raster-order k/v need as many key blocks as query blocks")
+    _lib.require_gpu(q, k, v, out, q_map, kv_map)
+    sel, cnt, maxk = build_csr(keep) if index is None else index
     if H != heads:
         raise ValueError(f"block mask has {H} heads, tensors have {heads}")
     _lib.require_gpu(sel, cnt)
@@ -98,6 +113,18 @@ def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, 
         raise ValueError("out is required")
     _lib.require_dtype(out, torch.bfloat16, "out")
     o_strides = o_strides or q_strides
+    if window is not None:
+        _check_extent(q, NQ * BLOCK, *q_strides, heads, head_dim, "q")
+        _check_extent(out, NQ * BLOCK, *o_strides, heads, head_dim, "out")
+        _check_extent(k, NK * BLOCK, *kv_strides, heads, head_dim, "k")
+        _check_extent(v, NK * BLOCK, *kv_strides, heads, head_dim, "v")
+        rc = _lib.lib().fvsr_bsa_fwd_window(
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            q_strides[0], q_strides[1], kv_strides[0], kv_strides[1], o_strides[0], o_strides[1],
+            sel.data_ptr(), cnt.data_ptr(), maxk, H, NQ, NK, head_dim, float(sm_scale),
+            frames, height, width, int(bool(kv_raster)), _lib.stream(q))
+        _lib.check(rc, "block_sparse_attention")
+        return out
     if (q_map is None) != (kv_map is None):
         raise ValueError("token maps come in pairs (q_map with kv_map)")
     if q_map is None:
@@ -117,6 +144,35 @@ def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, 
         sel.data_ptr(), cnt.data_ptr(), maxk, H, NQ, NK, head_dim, float(sm_scale),
         _lib.ptr(q_map), _lib.ptr(kv_map), _lib.stream(q))
     _lib.check(rc, "block_sparse_attention")
+    return out
+
+
+def dense_attention_strided(q, k, v, sm_scale=None, *, heads: int, head_dim: int, q_strides,
+                            kv_strides, out, o_strides=None):
+    """softmax(Q K^T * sm_scale) V per head over all keys (fvsr_attn_dense):
+    the attention with every key block kept, for the cross-attention over
+    the cached prompt (integrate.py:132-143).  q/out hold a multiple of 128
+    query tokens, k/v a multiple of 128 key tokens, at the given (token,
+    head) strides in elements; no block index is involved."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out")):
+        _lib.require_dtype(t, torch.bfloat16, n)
+    Lq, Lk = q.shape[0], k.shape[0]
+    if Lq % BLOCK or Lk % BLOCK or v.shape[0] != Lk or out.shape[0] != Lq:
+        raise ValueError(f"dense attention needs multiples of {BLOCK} tokens: q {Lq}, k {Lk}, "
+                         f"v {v.shape[0]}, out {out.shape[0]}")
+    o_strides = o_strides or q_strides
+    _check_extent(q, Lq, *q_strides, heads, head_dim, "q")
+    _check_extent(out, Lq, *o_strides, heads, head_dim, "out")
+    _check_extent(k, Lk, *kv_strides, heads, head_dim, "k")
+    _check_extent(v, Lk, *kv_strides, heads, head_dim, "v")
+    _lib.require_gpu(q, k, v, out)
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(head_dim)
+    rc = _lib.lib().fvsr_attn_dense(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), q_strides[0], q_strides[1],
+        kv_strides[0], kv_strides[1], o_strides[0], o_strides[1], heads, Lq // BLOCK,
+        Lk // BLOCK, head_dim, float(sm_scale), _lib.stream(q))
+    _lib.check(rc, "dense_attention")
     return out
 
 

@@ -281,6 +281,42 @@ int fvsr_bsa_fwd(const void* q, const void* k, const void* v, void* o, int64_t q
                  int64_t head_dim, float sm_scale, const int32_t* q_map, const int32_t* kv_map,
                  void* stream);
 
+/*
+ * fvsr_bsa_fwd with the window partition in closed form instead of token maps:
+ * the same attention (lcsa/triton_lcsa.py:19-61,74-94) on q/k/v that the
+ * reference's self-attention first permutes with WindowPartition3D
+ * (integrate.py:70-94, lcsa/reference.py:15-21; windows of 2 x 8 x 8 tokens).
+ * q and o rows are the raster tokens of a (frames, height, width) latent grid;
+ * query block i is window i: its slot s = (f*8 + y)*8 + x is token
+ * ((2*wf + f)*height + 8*wy + y)*width + 8*wx + x of window (wf, wy, wx).
+ * kv_raster = 1: k and v rows are raster tokens of the same grid, key block j =
+ * window j (NK == NQ); kv_raster = 0: k and v rows are already in window order
+ * (row = block position, e.g. a window-ordered K/V cache), NK blocks.
+ * No map is read: token rows are computed, so the first K/V loads of a block
+ * wait on no other load.  Requires frames % 2 == 0, height % 8 == 0,
+ * width % 8 == 0, frames*height*width == NQ*128, plus fvsr_bsa_fwd's
+ * requirements.
+ */
+int fvsr_bsa_fwd_window(const void* q, const void* k, const void* v, void* o,
+                        int64_t q_tok_stride, int64_t q_head_stride, int64_t kv_tok_stride,
+                        int64_t kv_head_stride, int64_t o_tok_stride, int64_t o_head_stride,
+                        const int32_t* sel, const int32_t* cnt, int64_t maxk, int64_t H,
+                        int64_t NQ, int64_t NK, int64_t head_dim, float sm_scale, int64_t frames,
+                        int64_t height, int64_t width, int kv_raster, void* stream);
+
+/*
+ * Dense attention: fvsr_bsa_fwd with every key block kept for every query
+ * block, for the cross-attention's softmax(Q K^T * sm_scale) V over the
+ * prompt K/V cached by init_cross_kv (integrate.py:132-143; upstream
+ * self.attn(q, cache_k, cache_v)).  NQ*128 query tokens, NK*128 key tokens,
+ * strides as in fvsr_bsa_fwd, no block index and no token map.  One
+ * workgroup of 8 waves takes two query blocks over one K/V stream.
+ */
+int fvsr_attn_dense(const void* q, const void* k, const void* v, void* o, int64_t q_tok_stride,
+                    int64_t q_head_stride, int64_t kv_tok_stride, int64_t kv_head_stride,
+                    int64_t o_tok_stride, int64_t o_head_stride, int64_t H, int64_t NQ,
+                    int64_t NK, int64_t head_dim, float sm_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -712,6 +712,111 @@ def test_bsa_empty_rows_and_token_maps(ops):
     assert (got[128:256, 0] == 0).all()
 
 
+@pytest.mark.parametrize("kv_raster", [True, False])
+def test_bsa_window_grid(ops, kv_raster):
+    """fvsr_bsa_fwd_window (the (2, 8, 8) window order computed from the
+    latent grid) against the gathered-map entry on the same data, bit for
+    bit, and against the float64 oracle on the window partition
+    (integrate.py:70-94).  Grid 4 x 16 x 24: two frame pairs of 2 x 3 windows,
+    so a swapped row/column index would show.  kv_raster: q, k, v are column
+    slices of one fused raster [L, 3*H*D] tensor (the C5 block's layout);
+    otherwise k/v are a window-ordered buffer with 6 cached windows ahead of
+    the current ones (the enable() path's K/V cache)."""
+    from flashvsr_sm89_ops.block import window_token_map
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    H, D, f, h, w = 2, 128, 4, 16, 24
+    L, HD = f * h * w, H * D
+    NQ = L // 128
+    NK = NQ if kv_raster else NQ + 6
+    rng = np.random.default_rng(31 + kv_raster)
+    qr = O.bf16(rng.standard_normal((L, HD)).astype(np.float32))
+    tok = window_token_map(f, h, w).numpy()
+    if kv_raster:
+        kr = O.bf16(rng.standard_normal((L, HD)).astype(np.float32))
+        vr = O.bf16(rng.standard_normal((L, HD)).astype(np.float32))
+        kw, vw = kr[tok], vr[tok]
+        qkv = dev_bf16(O.bf16_bits(np.concatenate([qr, kr, vr], 1)))
+        q, k, v = qkv[:, :HD], qkv[:, HD:2 * HD], qkv[:, 2 * HD:]
+        kv_map = torch.from_numpy(tok).to(DEV)
+    else:
+        kw = O.bf16(rng.standard_normal((NK * 128, HD)).astype(np.float32))
+        vw = O.bf16(rng.standard_normal((NK * 128, HD)).astype(np.float32))
+        q = dev_bf16(O.bf16_bits(qr))
+        k, v = dev_bf16(O.bf16_bits(kw)), dev_bf16(O.bf16_bits(vw))
+        kv_map = torch.arange(NK * 128, dtype=torch.int32, device=DEV)
+    keep = O.random_block_mask(H, NQ, NK, 0.45, seed=11)
+    keep[1, 4] = False                                   # an empty row: zeros
+    index = ops.build_csr(torch.from_numpy(keep).to(DEV))
+    outs = []
+    for mode in ("window", "map"):
+        out = torch.full((L, HD), 7.0, dtype=torch.bfloat16, device=DEV)
+        extra = ({"window": (f, h, w, kv_raster)} if mode == "window" else
+                 {"q_map": torch.from_numpy(tok).to(DEV), "kv_map": kv_map})
+        block_sparse_attention_strided(q, k, v, None, None, heads=H, head_dim=D,
+                                       q_strides=(q.stride(0), D), kv_strides=(k.stride(0), D),
+                                       out=out, o_strides=(HD, D), index=index, **extra)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]), "window grid and token map read different rows"
+    ref = O.sparse_attention(qr[tok].reshape(-1, H, D), kw.reshape(-1, H, D),
+                             vw.reshape(-1, H, D), keep)
+    got = host_f(outs[0]).reshape(L, H, D)[tok]           # raster rows -> window order
+    _attn_check(got, ref)
+    assert (got[4 * 128:5 * 128, 1] == 0).all()
+
+
+@pytest.mark.parametrize("nq,nk", [(5, 4), (2, 1)])
+def test_dense_attention_equals_all_kept_index(ops, nq, nk):
+    """fvsr_attn_dense (two query blocks per 8-wave workgroup, no index)
+    against fvsr_bsa_fwd with an all-kept block index on the same data: the
+    per-wave arithmetic is the same, so the outputs are equal bit for bit;
+    odd nq leaves the last pair's second block past the end (nothing may be
+    written there: the rows after the output stay as they were).  q is a
+    column slice of a wider tensor."""
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import (block_sparse_attention_strided,
+                                                 dense_attention_strided)
+    H, D = 3, 128
+    rng = np.random.default_rng(40 + nq)
+    qw = dev_bf16(O.bf16_bits(rng.standard_normal((nq * 128, 2 * H * D)).astype(np.float32)))
+    q = qw[:, H * D:]
+    k = dev_bf16(O.bf16_bits(rng.standard_normal((nk * 128, H * D)).astype(np.float32)))
+    v = dev_bf16(O.bf16_bits(rng.standard_normal((nk * 128, H * D)).astype(np.float32)))
+    keep = torch.ones(H, nq, nk, dtype=torch.bool, device=DEV)
+    a = torch.full(((nq + 1) * 128, H * D), 3.0, dtype=torch.bfloat16, device=DEV)
+    b = torch.full_like(a, 3.0)
+    block_sparse_attention_strided(q, k, v, keep, None, heads=H, head_dim=D,
+                                   q_strides=(2 * H * D, D), kv_strides=(H * D, D),
+                                   out=a[:nq * 128], o_strides=(H * D, D))
+    dense_attention_strided(q, k, v, None, heads=H, head_dim=D, q_strides=(2 * H * D, D),
+                            kv_strides=(H * D, D), out=b[:nq * 128], o_strides=(H * D, D))
+    assert torch.equal(a, b)
+    assert (b[nq * 128:] == 3.0).all()
+    ref = O.dense_attention(host_f(q).reshape(-1, H, D), host_f(k).reshape(-1, H, D),
+                            host_f(v).reshape(-1, H, D))
+    _attn_check(host_f(b[:nq * 128]).reshape(-1, H, D), ref)
+
+
+def test_bsa_output_row_alignment(ops):
+    """Output rows 16-byte aligned leave through LDS as whole rows; rows only
+    8-byte aligned (an out view starting 4 elements in) take the per-lane
+    stores: both give the same values."""
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    H, D, NQ, NK = 2, 128, 2, 3
+    rng = np.random.default_rng(44)
+    q = dev_bf16(O.bf16_bits(rng.standard_normal((NQ * 128, H * D)).astype(np.float32)))
+    k = dev_bf16(O.bf16_bits(rng.standard_normal((NK * 128, H * D)).astype(np.float32)))
+    v = dev_bf16(O.bf16_bits(rng.standard_normal((NK * 128, H * D)).astype(np.float32)))
+    keep = torch.from_numpy(O.random_block_mask(H, NQ, NK, 0.6, seed=3)).to(DEV)
+    outs = []
+    for off in (0, 4):
+        buf = torch.zeros(NQ * 128 * (H * D + 4) + 8, dtype=torch.bfloat16, device=DEV)
+        o = buf[off:off + NQ * 128 * (H * D + 4)].view(NQ * 128, H * D + 4)[:, :H * D]
+        block_sparse_attention_strided(q, k, v, keep, None, heads=H, head_dim=D,
+                                       q_strides=(H * D, D), kv_strides=(H * D, D), out=o,
+                                       o_strides=(H * D + 4, D))
+        outs.append(o.clone())
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("order", ["growing", "shrinking"])
 def test_bsa_running_max_moves_every_block(ops, order):
     """Key block j scaled by 2(j+1) (or in reverse): the largest score grows

@@ -855,3 +855,37 @@ def test_enable_rewrites_old_format_fp8_weights(tmp_path, monkeypatch):
     monkeypatch.setenv("FS89_FP8_WEIGHTS", other)
     with pytest.raises(ValueError, match="not a"):
         f.enable(pipe2, dit_module=make_fake_dit(), verbose=False)
+
+
+def test_bsa_window_entry_argument_checks():
+    """fvsr_bsa_fwd_window rejects a grid that is not whole (2, 8, 8)
+    windows covering NQ blocks, and raster k/v with NK != NQ, before anything
+    is launched (so fake pointers are never touched); the Python wrapper
+    raises ValueError for the same cases."""
+    from flashvsr_sm89_ops import _lib
+    from flashvsr_sm89_ops.lcsa.hip_lcsa import block_sparse_attention_strided
+    L = _lib.lib()
+    p = 16
+
+    def call(frames, height, width, NQ=12, NK=12, kv_raster=1, H=2):
+        return L.fvsr_bsa_fwd_window(p, p, p, p, 256, 128, 256, 128, 256, 128, p, p, NK, H, NQ,
+                                     NK, 128, 0.1, frames, height, width, kv_raster, None)
+    assert call(3, 16, 24) == _lib.FVSR_EINVAL           # odd frame count
+    assert call(4, 12, 24) == _lib.FVSR_EINVAL           # height not a multiple of 8
+    assert call(4, 16, 20) == _lib.FVSR_EINVAL           # width not a multiple of 8
+    assert call(4, 16, 32) == _lib.FVSR_EINVAL           # 16 windows, NQ = 12
+    assert call(4, 16, 24, NK=13) == _lib.FVSR_EINVAL    # raster k/v: NK must equal NQ
+    assert call(4, 16, 24, NQ=0, NK=0) == _lib.FVSR_EINVAL
+    assert call(0, 16, 24, NQ=0, NK=0, H=2) == _lib.FVSR_OK   # nothing to do
+    bf = torch.bfloat16
+    q = torch.zeros(1536, 256, dtype=bf)
+    sel = torch.zeros(2, 12, 12, dtype=torch.int32)
+    cnt = torch.zeros(2, 12, dtype=torch.int32)
+    with pytest.raises(ValueError, match="window grid"):
+        block_sparse_attention_strided(q, q, q, None, heads=2, head_dim=128, q_strides=(256, 128),
+                                       kv_strides=(256, 128), out=q, index=(sel, cnt, 12),
+                                       window=(4, 16, 32, True))
+    with pytest.raises(ValueError, match="not both"):
+        block_sparse_attention_strided(q, q, q, None, heads=2, head_dim=128, q_strides=(256, 128),
+                                       kv_strides=(256, 128), out=q, index=(sel, cnt, 12),
+                                       window=(4, 16, 24, True), q_map=cnt, kv_map=cnt)
