@@ -711,7 +711,14 @@ def main():
                          "counters (" + " ".join(MFMA_COUNTERS) + ") into JSON and exit")
     ap.add_argument("--blaslt", action="store_true",
                     help="time torch._scaled_mm (hipBLASLt) at the BASELINE GEMM shapes and exit")
+    ap.add_argument("--ktrace-from", metavar="CSV",
+                    help="summarise a rocprofv3 --kernel-trace kernel_trace.csv per kernel and "
+                         "grid size (the GEMM shapes share one kernel name) as a markdown table "
+                         "and exit")
     args = ap.parse_args()
+    if args.ktrace_from:
+        print(summarize_ktrace(args.ktrace_from))
+        return
     if args.traffic_from:
         print(json.dumps(summarize_traffic(*args.traffic_from, args.copy_probe_mib), indent=1))
         return
@@ -766,10 +773,20 @@ def main():
 # stack whose dispatches can be told apart in a counter file.  The GEMMs run
 # persistent grids of one workgroup per CU, so their dispatches share a name
 # and a grid and are not listed.
+# op -> (kernel name fragment, grid size in threads or None).  The GEMMs share
+# one kernel and differ by persistent grid (256 CUs: qkv 240 workgroups, ffn0
+# 232; o and ffn2 both 200, so their counters are averaged together).
 OP_KERNELS = {
-    "bsa": ("bsa_fwd_kernel<true>", None),
-    "gelu_quant": ("quant_rows_gelu_table", None),
+    "ln_modulate_quant": ("ln_modulate_row<false, true, false>", None),
+    "gemm_qkv": ("gemm_fp8_ring<0, true, 4>", 240 * 256),
     "rms_rope_qk": ("rms_rope_qk_vec", None),
+    "bsa": ("bsa_fwd_kernel<2, 2, false>", None),
+    "quant_attn": ("quant_rows_vec<3, false>", None),
+    "gemm_o_and_ffn2": ("gemm_fp8_ring<0, true, 4>", 200 * 256),
+    "gate_add_ln_modulate_quant": ("ln_modulate_row<false, true, true>", None),
+    "gemm_ffn0": ("gemm_fp8_ring<0, true, 4>", 232 * 256),
+    "gelu_quant": ("quant_rows_gelu_table", None),
+    "gate_add": ("gate_add_vec", None),
 }
 
 
@@ -813,6 +830,29 @@ def summarize_traffic(fetch_csv, write_csv, copy_mib):
 MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_VALU_MFMA_MOPS_F8",
                  "SQ_INSTS_VALU_MFMA_MOPS_BF16", "GRBM_GUI_ACTIVE")
 MFMA_KERNELS = {"gemm_fp8": "gemm_fp8", "bsa": "bsa_fwd_kernel"}
+
+
+def summarize_ktrace(csv_path, top=24):
+    """Per (kernel, workgroups) dispatch count and duration statistics of a
+    rocprofv3 kernel_trace.csv, largest total time first, as markdown."""
+    import csv
+    groups = {}
+    with open(csv_path) as fh:
+        for r in csv.DictReader(fh):
+            wg = int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"]))
+            name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+            name = name[5:] if name.startswith("void ") else name
+            key = (name.split("(")[0][:90], wg)
+            groups.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    total = sum(sum(v) for v in groups.values())
+    rows = sorted(groups.items(), key=lambda kv: -sum(kv[1]))[:top]
+    out = ["| kernel | workgroups | calls | avg us | median us | min us | max us | % time |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (name, wg), d in rows:
+        d = sorted(d)
+        out.append(f"| `{name}` | {wg} | {len(d)} | {sum(d) / len(d):.1f} | {d[len(d) // 2]:.1f} | "
+                   f"{d[0]:.1f} | {d[-1]:.1f} | {100 * sum(d) / total:.2f} |")
+    return "\n".join(out)
 
 
 def summarize_mfma(csv_path, simds=1024, xcds=8):
