@@ -247,6 +247,7 @@ FVSR_DEV int swz128(int r, int c) { return c ^ (r & 7) ^ ((r >> 3) & 1); }
 template <int MJ>
 struct DmaOffs {
   uint32_t a[Tile<MJ>::kLoadsA], b[8];
+  uint32_t ta, tb;  // L2 prefetch (long K): row starts of this lane's A row and B row
 };
 
 template <int MJ>
@@ -265,6 +266,12 @@ FVSR_DEV void dma_offsets(DmaOffs<MJ>& o, int64_t m0, int64_t n0, int64_t M, int
     const int r = wave * 64 + t * 8 + rl;
     const int64_t gb = n0 + r < N ? n0 + r : N - 1;
     o.b[t] = (uint32_t)(gb * ldb + swz128(r, c) * 16);
+  }
+  {
+    const int64_t ra = m0 + wave * (Tile<MJ>::TM / 4) + lane % (Tile<MJ>::TM / 4);
+    const int64_t rb = n0 + wave * 64 + lane;
+    o.ta = (uint32_t)((ra < M ? ra : M - 1) * lda);
+    o.tb = (uint32_t)((rb < N ? rb : N - 1) * ldb);
   }
 }
 
@@ -325,7 +332,26 @@ constexpr int kWaitVm0 = waitcnt_imm(0, 15);
 struct RingCtx {
   i32x4_t ra, rb;
   int wave, wm, wn, lane;
+  int kmax;               // K offset of the last pair
+  uint8_t LDS_AS* touch;  // 512 bytes of LDS that nothing reads
 };
+
+// Long K (ffn2, K = 8960): the operand panels are used by few tiles, so most
+// pair loads miss L2, and the two LDS pair slots put them only one pair ahead
+// of the MFMAs.  Each pair step also fetches, into a dummy LDS word, the
+// first 4 bytes of this lane's A row and B row two pairs further on: the
+// 128-byte lines land in L2 ahead of the pair's own loads.  Exactly two such
+// loads follow every pair's loads, so a pair is waited for with vmcnt(2).
+// (ffn2 218 -> 208 us; at K = 1536 the panels stay in L2 and the extra loads
+// cost 5-8%, so they are only issued for K >= 4096.)
+constexpr int kTouchAhead = 2;
+template <int MJ>
+FVSR_DEV void touch_pairs(const RingCtx& c, const DmaOffs<MJ>& o, int k0) {
+  const int kt = min(k0 + kTouchAhead * 128, c.kmax);
+  fvsr_buffer_load_lds(c.ra, (void LDS_AS*)c.touch, 4, __builtin_bit_cast(int, o.ta), kt, 0, 0);
+  fvsr_buffer_load_lds(c.rb, (void LDS_AS*)(c.touch + 256), 4, __builtin_bit_cast(int, o.tb), kt,
+                       0, 0);
+}
 
 // One 64-byte K step s of a tile (fragments of s in fa/fb):
 //   PAIR (s odd): wait until this wave's loads of the next pair (steps s+1,
@@ -356,17 +382,18 @@ FVSR_DEV void sched_step(std::integer_sequence<int, Q...>) {
   (sched_slot<PAIR, NM, NL, ND, Q>(), ...);
 }
 
-template <int MJ, bool PAIR, int RH, bool ZERO>
+template <int MJ, bool PAIR, int RH, bool ZERO, bool TOUCH>
 FVSR_DEV void ring_step(const RingCtx& c, const DmaOffs<MJ>& o, int k0, const uint8_t LDS_AS* rd,
                         uint8_t LDS_AS* ds, v16f (&acc)[4][MJ], const v8i (&fa)[MJ],
                         const v8i (&fb)[4], v8i (&na)[MJ], v8i (&nb)[4]) {
   __builtin_amdgcn_sched_barrier(0);  // nothing (MFMAs included) moves across a step boundary
   if (PAIR) {
-    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(TOUCH ? 2 : 0, 0));
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");  // no LDS access may move across the barrier
     __builtin_amdgcn_sched_barrier(0);
     issue_pair(ds, c.ra, c.rb, k0, o, c.wave);
+    if (TOUCH) touch_pairs<MJ>(c, o, k0);
   }
   read_step<MJ>(rd, RH, c.wm, c.wn, c.lane, na, nb);
   if (ZERO) {
@@ -666,7 +693,7 @@ FVSR_DEV void tile_origin(int t, int tiles_m, int tiles_n, int tile_rows, int64_
 // wave).  After a workgroup's last tile the same stream re-fetches that
 // tile's first pairs (harmless) and the workgroup drains its loads before it
 // exits.
-template <int EPI, bool DIRECT, int MJ>
+template <int EPI, bool DIRECT, int MJ, bool TOUCH = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(1, 1)))
 void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __restrict__ B,
                    int64_t ldb, int64_t M, int64_t N, int64_t K, EpiArgs ep) {
@@ -675,6 +702,7 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
   __shared__ __attribute__((aligned(1024))) uint8_t pair0[Tile<MJ>::kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t pair1[Tile<MJ>::kPairBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t spare[4 * kEpiWaveBytes];
+  __shared__ __attribute__((aligned(256))) uint8_t touch_lds[TOUCH ? 512 : 4];
   uint8_t LDS_AS* p0 = (uint8_t LDS_AS*)pair0;
   uint8_t LDS_AS* p1 = (uint8_t LDS_AS*)pair1;
 
@@ -690,15 +718,17 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
   uint8_t LDS_AS* prm = epa + kEpiStageBytes;
   const int KT = (int)(K / 64);
 
-  RingCtx c{make_rsrc(A), make_rsrc(B), wave, wm, wn, lane};
+  RingCtx c{make_rsrc(A), make_rsrc(B), wave, wm, wn, lane, (int)K - 128,
+            (uint8_t LDS_AS*)touch_lds};
   int64_t m0, n0;
   tile_origin(t, tiles_m, tiles_n, TM, m0, n0);
   DmaOffs<MJ> cur;
   dma_offsets<MJ>(cur, m0, n0, M, N, lda, ldb, wave, lane);
   issue_pair<MJ>(p0, c.ra, c.rb, 0, cur, wave);
   issue_pair<MJ>(p1, c.ra, c.rb, 128, cur, wave);
+  if (TOUCH) touch_pairs<MJ>(c, cur, 128);
   // The first pair (the older half of the loads in flight) has landed.
-  __builtin_amdgcn_s_waitcnt(waitcnt_imm(Tile<MJ>::kLoadsA + 8, 15));
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(Tile<MJ>::kLoadsA + 8 + (TOUCH ? 2 : 0), 15));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
   v16f acc[4][MJ];
@@ -707,16 +737,16 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
 
   for (;;) {
     // First trip: steps 0-3 (accumulators start from 0 at step 0).
-    ring_step<MJ, false, 1, true>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
-    ring_step<MJ, true, 0, false>(c, cur, 2 * 128, p1, p0, acc, na, nb, fa, fb);
-    ring_step<MJ, false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
-    ring_step<MJ, true, 0, false>(c, cur, 3 * 128, p0, p1, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, true, TOUCH>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false, TOUCH>(c, cur, 2 * 128, p1, p0, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, false, TOUCH>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false, TOUCH>(c, cur, 3 * 128, p0, p1, acc, na, nb, fa, fb);
     // Steady state: steps kt .. kt+3 load pairs kt/2 + 2 and kt/2 + 3.
     for (int kt = 4; kt < KT - 4; kt += 4) {
-      ring_step<MJ, false, 1, false>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
-      ring_step<MJ, true, 0, false>(c, cur, (kt + 4) * 64, p1, p0, acc, na, nb, fa, fb);
-      ring_step<MJ, false, 1, false>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
-      ring_step<MJ, true, 0, false>(c, cur, (kt + 6) * 64, p0, p1, acc, na, nb, fa, fb);
+      ring_step<MJ, false, 1, false, TOUCH>(c, cur, 0, p0, p0, acc, fa, fb, na, nb);
+      ring_step<MJ, true, 0, false, TOUCH>(c, cur, (kt + 4) * 64, p1, p0, acc, na, nb, fa, fb);
+      ring_step<MJ, false, 1, false, TOUCH>(c, cur, 0, p1, p1, acc, fa, fb, na, nb);
+      ring_step<MJ, true, 0, false, TOUCH>(c, cur, (kt + 6) * 64, p0, p1, acc, na, nb, fa, fb);
     }
     // Last trip: steps KT-4 .. KT-1; their loads are the next tile's pairs 0
     // and 1 and the last reads are the next tile's step 0.
@@ -728,10 +758,10 @@ void gemm_fp8_ring(const uint8_t* __restrict__ A, int64_t lda, const uint8_t* __
     // This tile's epilogue parameters load under the last trip's MFMAs.
     EpiParamRegs epr;
     fetch_epi_params(epr, ep, m0, n0, M, N, wm, wn, TM / 2, lane);
-    ring_step<MJ, false, 1, false>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
-    ring_step<MJ, true, 0, false>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
-    ring_step<MJ, false, 1, false>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
-    ring_step<MJ, true, 0, false>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, false, TOUCH>(c, nxt, 0, p0, p0, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false, TOUCH>(c, nxt, 0, p1, p0, acc, na, nb, fa, fb);
+    ring_step<MJ, false, 1, false, TOUCH>(c, nxt, 0, p1, p1, acc, fa, fb, na, nb);
+    ring_step<MJ, true, 0, false, TOUCH>(c, nxt, 128, p0, p1, acc, na, nb, fa, fb);
 
     // Epilogue (fa/fb now hold the next tile's step-0 fragments): passes of
     // 32 rows x 64 columns through the wave's own staging area.
@@ -868,14 +898,19 @@ void gemm_fp8_generic(const uint8_t* __restrict__ A, int64_t lda, const uint8_t*
 }
 
 enum class Path { kGeneric, kRing, kRingFast, kRingFast128 };
+constexpr int64_t kTouchMinK = 4096;  // L2 prefetch of the pair loads from this K on
 
 template <int EPI>
 void launch(Path path, unsigned grid, hipStream_t st, const uint8_t* a, int64_t lda,
             const uint8_t* b, int64_t ldb, int64_t M, int64_t N, int64_t K, const EpiArgs& ep) {
   if constexpr (EPI != FVSR_EPI_GATE_ADD) {  // gate-add keeps the general epilogue
     if (path == Path::kRingFast) {
-      hipLaunchKernelGGL((gemm_fp8_ring<EPI, true, 4>), dim3(grid), dim3(kThreads), 0, st, a, lda,
-                         b, ldb, M, N, K, ep);
+      if (K >= kTouchMinK)
+        hipLaunchKernelGGL((gemm_fp8_ring<EPI, true, 4, true>), dim3(grid), dim3(kThreads), 0, st,
+                           a, lda, b, ldb, M, N, K, ep);
+      else
+        hipLaunchKernelGGL((gemm_fp8_ring<EPI, true, 4>), dim3(grid), dim3(kThreads), 0, st, a,
+                           lda, b, ldb, M, N, K, ep);
       return;
     }
     if (path == Path::kRingFast128) {

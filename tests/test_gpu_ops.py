@@ -330,7 +330,7 @@ def test_fp8_gemm_ring_shapes(ops, MNK):
 
 @pytest.mark.parametrize("epi", ["bias", "rowmax"])
 @pytest.mark.parametrize("MNK", [(4224, 1536, 1536), (77, 512, 512), (1000, 2560, 768),
-                                 (2100, 8960, 512)])
+                                 (2100, 8960, 512), (300, 512, 4352)])
 def test_fp8_gemm_direct_epilogue_rows_past_m(ops, MNK, epi):
     """Whole column tiles take the fast epilogue, whose stores of rows past M
     are dropped by the store descriptor's byte range: the output is a view of
