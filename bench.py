@@ -769,23 +769,21 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-# Kernel (name fragment, grid size in work-items or None) of each op of the C5
-# stack whose dispatches can be told apart in a counter file.  The GEMMs run
-# persistent grids of one workgroup per CU, so their dispatches share a name
-# and a grid and are not listed.
-# op -> (kernel name fragment, grid size in threads or None).  The GEMMs share
-# one kernel and differ by persistent grid (256 CUs: qkv 240 workgroups, ffn0
-# 232; o and ffn2 both 200, so their counters are averaged together).
+# op -> (kernel name fragment, grid size in threads or None) for each op of the
+# C5 stack whose dispatches can be told apart in a counter file.  qkv, o and
+# ffn0 share one GEMM kernel and differ by persistent grid (qkv 240 workgroups,
+# o 200, ffn0 232); ffn2 (K = 8960) runs the variant with the L2 prefetch.
 OP_KERNELS = {
     "ln_modulate_quant": ("ln_modulate_row<false, true, false>", None),
-    "gemm_qkv": ("gemm_fp8_ring<0, true, 4>", 240 * 256),
+    "gemm_qkv": ("gemm_fp8_ring<0, true, 4, false>", 240 * 256),
     "rms_rope_qk": ("rms_rope_qk_vec", None),
     "bsa": ("bsa_fwd_kernel<2, 2, false>", None),
     "quant_attn": ("quant_rows_vec<3, false>", None),
-    "gemm_o_and_ffn2": ("gemm_fp8_ring<0, true, 4>", 200 * 256),
+    "gemm_o": ("gemm_fp8_ring<0, true, 4, false>", 200 * 256),
     "gate_add_ln_modulate_quant": ("ln_modulate_row<false, true, true>", None),
-    "gemm_ffn0": ("gemm_fp8_ring<0, true, 4>", 232 * 256),
+    "gemm_ffn0": ("gemm_fp8_ring<0, true, 4, false>", 232 * 256),
     "gelu_quant": ("quant_rows_gelu_table", None),
+    "gemm_ffn2": ("gemm_fp8_ring<0, true, 4, true>", 200 * 256),
     "gate_add": ("gate_add_vec", None),
 }
 
