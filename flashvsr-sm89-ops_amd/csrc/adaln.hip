@@ -230,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_vec(
           *(u32x2_t*)(codes + row[r] * D + c * 8) = chunk_codes_fma(o[j], qr, fminf(qs, 3.40282347e38f));
         }
       }
-      if (lane == 0 && l0 + r < L) row_scale[row[r]] = amax / 448.0f;
+      if (lane == 0 && l0 + r < L) row_scale[row[r]] = act_scale(amax);
     }
   }
 }
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_row(
                     quot_signed(o[6], qr, qsf), quot_signed(o[7], qr, qsf));
       if (lane + 64 * j < nchunk) *(u32x2_t*)(codes + row * D + (lane + 64 * j) * 8) = q;
     }
-    if (lane == 0) row_scale[row] = amax / 448.0f;
+    if (lane == 0) row_scale[row] = act_scale(amax);
   }
 }
 
@@ -432,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_generic(
       codes[row * D + d] =
           (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(o / qs), 0.0f, 0, false) & 0xff);
     }
-    if (lane == 0) row_scale[row] = amax / 448.0f;
+    if (lane == 0) row_scale[row] = act_scale(amax);
   }
 }
 
@@ -548,7 +548,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_vec(
           *(u32x2_t*)(codes + row[r] * D + c * 8) = chunk_codes_fma(o[j], qr, fminf(qs, 3.40282347e38f));
         }
       }
-      if (lane == 0 && r0 + r < rows) row_scale[row[r]] = amax / 448.0f;
+      if (lane == 0 && r0 + r < rows) row_scale[row[r]] = act_scale(amax);
     }
   }
 }
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(kThreads) void layer_norm_generic(
       codes[row * D + d] =
           (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(o / qs), 0.0f, 0, false) & 0xff);
     }
-    if (lane == 0) row_scale[row] = amax / 448.0f;
+    if (lane == 0) row_scale[row] = act_scale(amax);
   }
 }
 

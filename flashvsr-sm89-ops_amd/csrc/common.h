@@ -52,6 +52,16 @@ FVSR_DEV uint32_t pack_e4m3x4(float a, float b, float c, float d) {
 
 FVSR_DEV float clamp448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 
+// The scale an activation quantisation returns, amax / 448 as torch computes
+// it on the GPU: the reference returns `amax / FP8_MAX` (a device tensor
+// divided by a Python float, flashvsr_sm89_ops/fp8_quant.py:54 and
+// fp8_ffn.py:72), which torch evaluates as amax * fl(1/448), its
+// reciprocal-multiply path for a host-scalar divisor.  That differs from the
+// IEEE quotient by one ulp for about half of all amax values.  (The scale the
+// codes are divided by, max(amax, 1e-12) / 448, is a true division inside the
+// reference's kernels and stays one here.)
+FVSR_DEV float act_scale(float amax) { return amax * (1.0f / 448.0f); }
+
 // Lane id, recomputed where it is used.  Address arithmetic derived from it
 // cannot be hoisted out of a loop by the compiler, which otherwise keeps a
 // loop-invariant offset per load alive (and spills them) for the whole loop.

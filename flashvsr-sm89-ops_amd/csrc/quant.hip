@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_vec(
                     quot_signed(f[j][4 * h + 2], r, sc), quot_signed(f[j][4 * h + 3], r, sc));
     if (c < nchunk) *(u32x2_t*)(qr + c * 8) = q;
   }
-  if (lane == 0) scale_out[row] = amax / 448.0f;
+  if (lane == 0) scale_out[row] = act_scale(amax);
 }
 
 // ---------------------------------------------------------------------------
@@ -181,7 +181,7 @@ FVSR_DEV void gelu_quant_row(const u32x4_t (&v)[VPL], const uint16_t* tab, int64
     const int c = min(lane + 64 * j, nchunk - 1);
     __builtin_nontemporal_store(q, (u32x2_t*)(qr + (uint32_t)c * 8u));
   }
-  if (lane == 0) scale_out[row] = amax / 448.0f;
+  if (lane == 0) scale_out[row] = act_scale(amax);
 }
 
 // Codes of one row's GELU values against a given scale (the per-tensor
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(kTabWaves * 64) void quant_tensor_gelu_table(
   const float amax = wave_max_abs(m);
   __syncthreads();
   const float s = qscale(amax), r = 1.0f / s, sc = qscale_fin(s);
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = amax / 448.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = act_scale(amax);
   const int nchunk = (int)(cols >> 3);
   const int64_t stride = (int64_t)gridDim.x * kTabWaves;
   u32x4_t v[VPL];
@@ -303,7 +303,7 @@ __global__ __launch_bounds__(kThreads) void quant_rows_generic(
     float q = clamp448(load_val<GELU>(xr + c) / s);
     qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
   }
-  if (lane == 0) scale_out[row] = amax / 448.0f;
+  if (lane == 0) scale_out[row] = act_scale(amax);
 }
 
 // ---------------------------------------------------------------------------
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
   __shared__ float red[kWaves];
   const float amax = reduce_partials(part, nparts, red);
   const float s = qscale(amax), r = 1.0f / s;
-  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = amax / 448.0f;
+  if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = act_scale(amax);
   const int lane = threadIdx.x & 63;
   for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
        row += (int64_t)gridDim.x * kWaves) {

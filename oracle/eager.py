@@ -26,13 +26,20 @@ BF = torch.bfloat16
 E4M3 = torch.float8_e4m3fn
 
 
+# fl(1/448): on the GPU torch divides a tensor by a Python float as a product
+# with the float reciprocal (the CPU divides), so the reference's returned
+# scale `amax / FP8_MAX` (fp8_quant.py:54) is amax * fl(1/448).
+_INV448 = torch.tensor(1.0 / 448.0, dtype=torch.float32)
+
+
 def q_act(x, per_token):
     """Activation quantisation (fp8_quant.py:26-35,54; per row for per-token):
-    s = max(amax, 1e-12)/448, e4m3(clamp(x/s, +-448)), returned scale amax/448."""
+    s = max(amax, 1e-12)/448, e4m3(clamp(x/s, +-448)), returned scale
+    amax/448 in the GPU's evaluation (amax * fl(1/448))."""
     xf = x.float()
     amax = xf.abs().amax(dim=1, keepdim=True) if per_token else xf.abs().amax().reshape(1, 1)
     s = amax.clamp(min=1e-12) / 448.0
-    return (xf / s).clamp(-448.0, 448.0).to(E4M3), amax / 448.0
+    return (xf / s).clamp(-448.0, 448.0).to(E4M3), amax * _INV448
 
 
 def q_weight(w, per_channel):

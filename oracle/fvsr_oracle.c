@@ -16,6 +16,10 @@
  *   orc_quant_rows    contract Q-A: amax -> s = max(amax,1e-12)/448 ->
  *                     e4m3(clamp(x/s, +-448)), returned scale amax/448
  *                     (fp8_quant.py:16-35,42-55), per tensor or per row.
+ *                     The returned scale is `amax / FP8_MAX` of a device
+ *                     tensor, which torch evaluates on the GPU as
+ *                     amax * fl(1/448) (reciprocal multiply for a host-scalar
+ *                     divisor), so that is the product formed here.
  *   orc_gelu_bf16     tanh-GELU through 1-2/(exp(2u)+1), rounded to bf16
  *                     (fp8_ffn.py:24-30), with orc_expf as the exp.
  *   orc_expf          fp32 exp by Cody-Waite reduction + degree-6 Taylor
@@ -149,7 +153,7 @@ void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
                 v = v > FP8_MAX ? FP8_MAX : v;
                 q[r * cols + c] = orc_e4m3_one(v);
             }
-        scale_out[g] = amax / FP8_MAX;
+        scale_out[g] = amax * (1.0f / FP8_MAX);
     }
 }
 

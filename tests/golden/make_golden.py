@@ -5,7 +5,8 @@ fixtures pin the oracle and the HIP path to torch's own eager CPU arithmetic
 for each op's stock math, i.e. what the reference kernels replace:
   quant_*      fp32 eager chain of the quantisation contract
                (flashvsr_sm89_ops/fp8_quant.py:26-35,54: amax, clamp(1e-12)/448,
-               x/s, clamp +-448, cast to float8_e4m3fn)
+               x/s, clamp +-448, cast to float8_e4m3fn); the returned scale
+               `amax / FP8_MAX` as torch evaluates it on the GPU (gpu_over_448)
   wq_*         weight quantisation eager expressions (fp8_linear.py:20-22) and
                their per-output-channel form
   gelu_*       F.gelu(approximate='tanh') in bf16 over every bf16 bit pattern
@@ -36,6 +37,15 @@ def codes(t: torch.Tensor) -> np.ndarray:
     return t.contiguous().view(torch.uint8).numpy().copy()
 
 
+def gpu_over_448(t: torch.Tensor) -> torch.Tensor:
+    """`t / 448.0` for an fp32 tensor as torch computes it on the GPU: a
+    tensor divided by a Python float is multiplied by the float reciprocal
+    there (fl(1/448)), whereas the CPU divides.  The reference's returned
+    scales (fp8_quant.py:54, fp8_ffn.py:72) are such a division of a device
+    tensor."""
+    return t * torch.tensor(1.0 / 448.0, dtype=torch.float32)
+
+
 def main():
     g = torch.Generator().manual_seed(20261201)
     out = {}
@@ -49,11 +59,11 @@ def main():
     s = torch.clamp(amax, min=1e-12) / 448.0
     out["quant_x"] = bits(x)
     out["quant_tensor_q"] = codes((xf / s).clamp(-448.0, 448.0).to(torch.float8_e4m3fn))
-    out["quant_tensor_s"] = (amax / 448.0).reshape(1).numpy()
+    out["quant_tensor_s"] = gpu_over_448(amax).reshape(1).numpy()
     amax_r = xf.abs().amax(dim=1, keepdim=True)
     s_r = torch.clamp(amax_r, min=1e-12) / 448.0
     out["quant_row_q"] = codes((xf / s_r).clamp(-448.0, 448.0).to(torch.float8_e4m3fn))
-    out["quant_row_s"] = (amax_r / 448.0).reshape(-1).numpy()
+    out["quant_row_s"] = gpu_over_448(amax_r).reshape(-1).numpy()
 
     # --- weight quantisation ---
     w = (torch.randn(96, 256, generator=g) * 0.02).to(torch.bfloat16)
@@ -77,7 +87,7 @@ def main():
     out["gq_h"] = bits(h)
     out["gq_row_q"] = codes((gq / (torch.clamp(ga, min=1e-12) / 448.0)).clamp(-448, 448)
                            .to(torch.float8_e4m3fn))
-    out["gq_row_s"] = (ga / 448.0).reshape(-1).numpy()
+    out["gq_row_s"] = gpu_over_448(ga).reshape(-1).numpy()
 
     # --- LayerNorm + modulate, gate_add ---
     B, L, D = 2, 16, 1536

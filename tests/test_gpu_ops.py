@@ -72,6 +72,11 @@ def test_quantize_fp8_bitexact(ops, shape, per_token):
     rq, rs = O.quantize_fp8(x, per_row=per_token)
     assert np.array_equal(host_codes(q), rq)
     assert np.array_equal(host_f(s).reshape(-1), rs)
+    # the returned scale is the reference's own expression `amax / FP8_MAX`
+    # (fp8_quant.py:54) as torch evaluates it on this GPU
+    xf = dev_bf16(x).float().abs()
+    amax = xf.amax(dim=1, keepdim=True) if per_token else xf.amax()
+    assert torch.equal(s.reshape(-1), (amax / 448.0).reshape(-1))
 
 
 def test_quantize_golden(ops):
