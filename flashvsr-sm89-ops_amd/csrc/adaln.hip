@@ -395,40 +395,42 @@ __global__ __launch_bounds__(kThreads) void ln_modulate_row(
   }
 }
 
-// Any D: three passes over the row from global memory (L2-resident after the first).
+// Any D and any input types (x, scale, shift of types xt, st, ht; out of
+// type xt): three passes over the row from global memory (L2-resident after
+// the first).
 __global__ __launch_bounds__(kThreads) void ln_modulate_generic(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ scale,
-    const uint16_t* __restrict__ shift, uint16_t* __restrict__ out, int64_t rows, int64_t L,
+    const void* __restrict__ x, int xt, const void* __restrict__ scale, int st,
+    const void* __restrict__ shift, int ht, void* __restrict__ out, int64_t rows, int64_t L,
     int64_t D, float eps, uint8_t* __restrict__ codes, float* __restrict__ row_scale) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + row * D;
+  const int64_t xr = row * D;
   float sum = 0.0f;
-  for (int64_t d = lane; d < D; d += 64) sum += bf2f(xr[d]);
+  for (int64_t d = lane; d < D; d += 64) sum += ld_elem(x, xt, xr + d);
   const float mean = wave_sum(sum) / (float)D;
   float sq = 0.0f;
   for (int64_t d = lane; d < D; d += 64) {
-    const float t = bf2f(xr[d]) - mean;
+    const float t = ld_elem(x, xt, xr + d) - mean;
     sq += t * t;
   }
   const float den = sqrtf(wave_sum(sq) / (float)D + eps);
   const int64_t pb = (row / L) * D;
   float amax = 0.0f;
   for (int64_t d = lane; d < D; d += 64) {
-    const float xn = round_bf16((bf2f(xr[d]) - mean) / den);
-    const float y = round_bf16(xn * round_bf16(1.0f + bf2f(scale[pb + d])));
-    const float o = round_bf16(y + bf2f(shift[pb + d]));
+    const float xn = round_bf16((ld_elem(x, xt, xr + d) - mean) / den);
+    const float y = round_bf16(xn * round_bf16(1.0f + ld_elem(scale, st, pb + d)));
+    const float o = round_bf16(y + ld_elem(shift, ht, pb + d));
     amax = fmaxf(amax, fabsf(o));
-    if (out) out[row * D + d] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffff);
+    if (out) st_elem(out, xt, xr + d, o);
   }
   if (codes) {
     amax = wave_max(amax);
     const float qs = fmaxf(amax, 1e-12f) / 448.0f;
     for (int64_t d = lane; d < D; d += 64) {
-      const float xn = round_bf16((bf2f(xr[d]) - mean) / den);
-      const float y = round_bf16(xn * round_bf16(1.0f + bf2f(scale[pb + d])));
-      const float o = round_bf16(y + bf2f(shift[pb + d]));
+      const float xn = round_bf16((ld_elem(x, xt, xr + d) - mean) / den);
+      const float y = round_bf16(xn * round_bf16(1.0f + ld_elem(scale, st, pb + d)));
+      const float o = round_bf16(y + ld_elem(shift, ht, pb + d));
       codes[row * D + d] =
           (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(clamp448(o / qs), 0.0f, 0, false) & 0xff);
     }
@@ -623,18 +625,21 @@ __global__ __launch_bounds__(kThreads) void gate_add_vec(
   }
 }
 
+// Any shape and input types (x, gate, res of types xt, gt, rt; out of type xt).
 __global__ __launch_bounds__(kThreads) void gate_add_generic(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate,
-    const uint16_t* __restrict__ res, uint16_t* __restrict__ out, int64_t n, int64_t LD,
+    const void* __restrict__ x, int xt, const void* __restrict__ gate, int gt,
+    const void* __restrict__ res, int rt, void* __restrict__ out, int64_t n, int64_t LD,
     int64_t D) {
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * kThreads) {
-    const float y = round_bf16(bf2f(gate[(i / LD) * D + (i % D)]) * bf2f(res[i]));
-    out[i] = (uint16_t)(pack_bf16x2(bf2f(x[i]) + y, 0.0f) & 0xffff);
+    const float y = round_bf16(ld_elem(gate, gt, (i / LD) * D + (i % D)) * ld_elem(res, rt, i));
+    st_elem(out, xt, i, round_bf16(ld_elem(x, xt, i) + y));
   }
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool dtype_ok(int dt) { return dt == FVSR_DT_BF16 || dt == FVSR_DT_F16 || dt == FVSR_DT_F32; }
 
 }  // namespace
 
@@ -679,8 +684,8 @@ extern "C" int fvsr_ln_modulate(const void* x, const void* scale, const void* sh
       hipLaunchKernelGGL((ln_modulate_vec<3, kLnRows, false, true>), vgrid, block, 0, st, xp, sp,
                          hp, op, B, L, D, eps, qp, row_scale);
   } else {
-    hipLaunchKernelGGL(ln_modulate_generic, grid, block, 0, st, xp, sp, hp, op, rows, L, D, eps,
-                       qp, row_scale);
+    hipLaunchKernelGGL(ln_modulate_generic, grid, block, 0, st, x, FVSR_DT_BF16, scale,
+                       FVSR_DT_BF16, shift, FVSR_DT_BF16, out, rows, L, D, eps, qp, row_scale);
   }
   return fvsr_launch_status();
 }
@@ -765,9 +770,12 @@ extern "C" int fvsr_gate_add_ln_modulate(const void* x, const void* gate, const 
   return fvsr_launch_status();
 }
 
-extern "C" int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out,
-                             int64_t B, int64_t L, int64_t D, void* stream) {
-  if (B < 0 || L < 0 || D <= 0) return FVSR_EINVAL;
+extern "C" int fvsr_gate_add_dt(const void* x, int x_dtype, const void* gate, int gate_dtype,
+                                const void* res, int res_dtype, void* out, int64_t B, int64_t L,
+                                int64_t D, void* stream) {
+  if (B < 0 || L < 0 || D <= 0 || !dtype_ok(x_dtype) || !dtype_ok(gate_dtype) ||
+      !dtype_ok(res_dtype))
+    return FVSR_EINVAL;
   const int64_t n = B * L * D;
   if (n == 0) return FVSR_OK;
   if (!x || !gate || !res || !out) return FVSR_EINVAL;
@@ -775,7 +783,9 @@ extern "C" int fvsr_gate_add(const void* x, const void* gate, const void* res, v
   const uint16_t *xp = (const uint16_t*)x, *gp = (const uint16_t*)gate,
                  *rp = (const uint16_t*)res;
   uint16_t* op = (uint16_t*)out;
-  const bool vec = D % 8 == 0 && aligned16(x) && aligned16(gate) && aligned16(res) &&
+  const bool bf16 = x_dtype == FVSR_DT_BF16 && gate_dtype == FVSR_DT_BF16 &&
+                    res_dtype == FVSR_DT_BF16;
+  const bool vec = bf16 && D % 8 == 0 && aligned16(x) && aligned16(gate) && aligned16(res) &&
                    aligned16(out);
   if (vec) {
     const int64_t nchunk = n / 8;
@@ -786,9 +796,33 @@ extern "C" int fvsr_gate_add(const void* x, const void* gate, const void* res, v
   } else {
     int64_t blocks = (n + kThreads - 1) / kThreads;
     if (blocks > 65536) blocks = 65536;
-    hipLaunchKernelGGL(gate_add_generic, dim3((unsigned)blocks), dim3(kThreads), 0, st, xp, gp,
-                       rp, op, n, L * D, D);
+    hipLaunchKernelGGL(gate_add_generic, dim3((unsigned)blocks), dim3(kThreads), 0, st, x,
+                       x_dtype, gate, gate_dtype, res, res_dtype, out, n, L * D, D);
   }
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out,
+                             int64_t B, int64_t L, int64_t D, void* stream) {
+  return fvsr_gate_add_dt(x, FVSR_DT_BF16, gate, FVSR_DT_BF16, res, FVSR_DT_BF16, out, B, L, D,
+                          stream);
+}
+
+extern "C" int fvsr_ln_modulate_dt(const void* x, int x_dtype, const void* scale, int scale_dtype,
+                                   const void* shift, int shift_dtype, void* out, int64_t B,
+                                   int64_t L, int64_t D, float eps, void* stream) {
+  if (B < 0 || L < 0 || D <= 0 || !dtype_ok(x_dtype) || !dtype_ok(scale_dtype) ||
+      !dtype_ok(shift_dtype))
+    return FVSR_EINVAL;
+  if (x_dtype == FVSR_DT_BF16 && scale_dtype == FVSR_DT_BF16 && shift_dtype == FVSR_DT_BF16)
+    return fvsr_ln_modulate(x, scale, shift, out, B, L, D, eps, nullptr, nullptr, stream);
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!x || !scale || !shift || !out) return FVSR_EINVAL;
+  hipLaunchKernelGGL(ln_modulate_generic, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
+                     dim3(kThreads), 0, (hipStream_t)stream, x, x_dtype, scale, scale_dtype,
+                     shift, shift_dtype, out, rows, L, D, eps, (uint8_t*)nullptr,
+                     (float*)nullptr);
   return fvsr_launch_status();
 }
 

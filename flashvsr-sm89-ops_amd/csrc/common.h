@@ -62,6 +62,41 @@ FVSR_DEV float clamp448(float v) { return fminf(fmaxf(v, -448.0f), 448.0f); }
 // reference's kernels and stays one here.)
 FVSR_DEV float act_scale(float amax) { return amax * (1.0f / 448.0f); }
 
+// Element access of the dtype-generic kernels (FVSR_DT_* codes, uniform per
+// launch).  Loads widen to fp32 exactly, as the reference's kernels load every
+// input with .to(tl.float32).  st_elem takes a result already rounded to bf16
+// (every output of these ops is) and writes it in the tensor's type: exactly
+// for bf16 and fp32, rounded to nearest even for fp16 (v_cvt_f16_f32).
+FVSR_DEV float ld_elem(const void* p, int dt, int64_t i) {
+  if (dt == FVSR_DT_F32) return ((const float*)p)[i];
+  if (dt == FVSR_DT_F16) return (float)((const _Float16*)p)[i];
+  return bf2f(((const uint16_t*)p)[i]);
+}
+FVSR_DEV void st_elem(void* p, int dt, int64_t i, float v) {
+  if (dt == FVSR_DT_F32)
+    ((float*)p)[i] = v;
+  else if (dt == FVSR_DT_F16)
+    ((_Float16*)p)[i] = (_Float16)v;
+  else
+    ((uint16_t*)p)[i] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xffff);
+}
+// v rounded to the precision of type dt (nearest even), as fp32.
+FVSR_DEV float round_to(int dt, float v) {
+  if (dt == FVSR_DT_F32) return v;
+  if (dt == FVSR_DT_F16) return (float)(_Float16)v;
+  return round_bf16(v);
+}
+
+// torch's fp32 -> float8_e4m3fn cast: round to nearest even, magnitudes above
+// 464 (and NaN) give the NaN code 0x7F with the value's sign (e4m3fn has no
+// infinity); v_cvt_pk_fp8_f32 gives the same codes up to 464 but 0xFF for
+// every NaN.
+FVSR_DEV uint8_t e4m3_cast(float v) {
+  const uint32_t u = __float_as_uint(v);
+  if (!(fabsf(v) <= 464.0f)) return (uint8_t)(((u >> 24) & 0x80u) | 0x7Fu);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xff);
+}
+
 // Lane id, recomputed where it is used.  Address arithmetic derived from it
 // cannot be hoisted out of a loop by the compiler, which otherwise keeps a
 // loop-invariant offset per load alive (and spills them) for the whole loop.

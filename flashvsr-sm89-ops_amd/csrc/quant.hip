@@ -27,9 +27,11 @@ constexpr int kWaves = 4;            // wavefronts per workgroup
 constexpr int kThreads = kWaves * 64;
 constexpr int kMaxPartials = 1024;   // tensor-mode partial maxima
 
+// Element i of x (type dt, FVSR_DT_*) as fp32, or its tanh-GELU rounded to
+// bf16: the scalar paths, which also take fp16 and fp32 inputs.
 template <bool GELU>
-FVSR_DEV float load_val(const uint16_t* p) {
-  float v = bf2f(*p);
+FVSR_DEV float load_val(const void* x, int dt, int64_t i) {
+  const float v = ld_elem(x, dt, i);
   return GELU ? gelu_tanh_bf16(v) : v;
 }
 
@@ -285,22 +287,23 @@ __global__ __launch_bounds__(kRowTabWaves * 64) void quant_rows_gelu_table(
   }
 }
 
-// Row mode, any shape: two passes over the row (the second hits L2).
+// Row mode, any shape and input type: two passes over the row (the second
+// hits L2).  The codes are those of the IEEE quotient v / s.
 template <bool GELU>
 __global__ __launch_bounds__(kThreads) void quant_rows_generic(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    const void* __restrict__ x, int dt, int64_t rows, int64_t cols, int64_t ld,
     uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + row * ld;
+  const int64_t xr = row * ld;
   float m = 0.0f;
-  for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(xr + c)));
+  for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(x, dt, xr + c)));
   const float amax = wave_max_abs(m);
   const float s = qscale(amax);
   uint8_t* qr = codes + row * cols;
   for (int64_t c = lane; c < cols; c += 64) {
-    float q = clamp448(load_val<GELU>(xr + c) / s);
+    float q = clamp448(load_val<GELU>(x, dt, xr + c) / s);
     qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
   }
   if (lane == 0) scale_out[row] = act_scale(amax);
@@ -320,24 +323,26 @@ FVSR_DEV float block_max(float m, float* red) {
 }
 
 // Partial |x| maxima: workgroup b covers rows b, b+G, ... (one wave per row).
+// VEC: bf16 rows in 16-byte chunks; otherwise element loads of type dt.
 template <bool GELU, bool VEC>
 __global__ __launch_bounds__(kThreads) void amax_partial(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    const void* __restrict__ x, int dt, int64_t rows, int64_t cols, int64_t ld,
     float* __restrict__ part) {
   __shared__ float red[kWaves];
   const int lane = threadIdx.x & 63;
   float m = 0.0f;
   for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
        row += (int64_t)gridDim.x * kWaves) {
-    const uint16_t* xr = x + row * ld;
     if (VEC) {
+      const uint16_t* xr = (const uint16_t*)x + row * ld;
       for (int64_t c = lane; c < (cols >> 3); c += 64) {
         u32x4_t v = *(const u32x4_t*)(xr + c * 8);
         if (GELU) v = gelu_chunk(v);
         m = fmaxf(m, chunk_absmax(v));
       }
     } else {
-      for (int64_t c = lane; c < cols; c += 64) m = fmaxf(m, fabsf(load_val<GELU>(xr + c)));
+      for (int64_t c = lane; c < cols; c += 64)
+        m = fmaxf(m, fabsf(load_val<GELU>(x, dt, row * ld + c)));
     }
   }
   m = block_max(m, red);
@@ -365,9 +370,12 @@ FVSR_DEV float reduce_partials(const float* __restrict__ part, int nparts, float
   return block_max(m, red);
 }
 
+// Codes against the tensor's scale (the partial maxima reduced again by every
+// workgroup).  VEC: bf16 rows in 16-byte chunks; otherwise element loads of
+// type dt and the IEEE quotient.
 template <bool GELU, bool VEC>
 __global__ __launch_bounds__(kThreads) void quant_tensor(
-    const uint16_t* __restrict__ x, int64_t rows, int64_t cols, int64_t ld,
+    const void* __restrict__ x, int dt, int64_t rows, int64_t cols, int64_t ld,
     const float* __restrict__ part, int nparts, uint8_t* __restrict__ codes,
     float* __restrict__ scale_out) {
   __shared__ float red[kWaves];
@@ -377,9 +385,9 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
   const int lane = threadIdx.x & 63;
   for (int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6); row < rows;
        row += (int64_t)gridDim.x * kWaves) {
-    const uint16_t* xr = x + row * ld;
     uint8_t* qr = codes + row * cols;
     if (VEC) {
+      const uint16_t* xr = (const uint16_t*)x + row * ld;
       for (int64_t c = lane; c < (cols >> 3); c += 64) {
         u32x4_t v = *(const u32x4_t*)(xr + c * 8);
         if (GELU) v = gelu_chunk(v);
@@ -387,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void quant_tensor(
       }
     } else {
       for (int64_t c = lane; c < cols; c += 64) {
-        float q = clamp448(load_val<GELU>(xr + c) / s);
+        float q = clamp448(load_val<GELU>(x, dt, row * ld + c) / s);
         qr[c] = (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(q, 0.0f, 0, false) & 0xff);
       }
     }
@@ -426,43 +434,49 @@ __global__ __launch_bounds__(kThreads) void gelu_amax_from_hmax(
 // ---------------------------------------------------------------------------
 // Static weight quantisation (fp8_linear.py:17-22 and its per-channel form).
 // ---------------------------------------------------------------------------
-FVSR_DEV float weight_scale(float amax) {
-  const float lo = round_bf16(1e-12f);
-  float s = round_bf16(amax / 448.0f);
-  return fmaxf(s, lo);
+// `(w.abs().amax() / FP8_MAX).clamp(min=1e-12).float()` evaluated in the
+// weight's type dt: the division by a Python float is amax * fl(1/448) on the
+// GPU, rounded to dt; the clamp compares in fp32 against 1e-12 rounded to dt
+// (0 in fp16) and keeps a NaN.  For bf16 weights t(amax * fl(1/448)) equals
+// t(amax / 448) for every amax (checked exhaustively on the host).
+FVSR_DEV float weight_scale(float amax, int dt) {
+  const float s = round_to(dt, amax * (1.0f / 448.0f));
+  const float lo = round_to(dt, 1e-12f);
+  return s < lo ? lo : s;
 }
 
-FVSR_DEV uint8_t weight_code(float w, float s, bool per_channel) {
-  float v = w / s;
-  if (!per_channel) v = round_bf16(v);
-  v = clamp448(v);  // |v| <= 450 after rounding; 450 -> 448 either way
-  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(v, 0.0f, 0, false) & 0xff);
+// Code of one weight element: per tensor, w / s is evaluated in the weight's
+// type (a 0-dim fp32 scale does not promote it) and rounded to dt before the
+// cast; per channel the [N, 1] fp32 scales promote the quotient to fp32.
+FVSR_DEV uint8_t weight_code(float w, float s, bool per_channel, int dt) {
+  const float v = w / s;
+  return e4m3_cast(per_channel ? v : round_to(dt, v));
 }
 
 __global__ __launch_bounds__(kThreads) void quant_weight_rows(
-    const uint16_t* __restrict__ w, int64_t n, int64_t k, uint8_t* __restrict__ codes,
+    const void* __restrict__ w, int dt, int64_t n, int64_t k, uint8_t* __restrict__ codes,
     float* __restrict__ scale_out) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= n) return;
-  const uint16_t* wr = w + row * k;
   float m = 0.0f;
-  for (int64_t c = lane; c < k; c += 64) m = fmaxf(m, fabsf(bf2f(wr[c])));
-  const float s = weight_scale(wave_max_abs(m));
-  for (int64_t c = lane; c < k; c += 64) codes[row * k + c] = weight_code(bf2f(wr[c]), s, true);
+  for (int64_t c = lane; c < k; c += 64) m = fmaxf(m, fabsf(ld_elem(w, dt, row * k + c)));
+  const float s = weight_scale(wave_max_abs(m), dt);
+  for (int64_t c = lane; c < k; c += 64)
+    codes[row * k + c] = weight_code(ld_elem(w, dt, row * k + c), s, true, dt);
   if (lane == 0) scale_out[row] = s;
 }
 
 __global__ __launch_bounds__(kThreads) void quant_weight_tensor(
-    const uint16_t* __restrict__ w, int64_t n, int64_t k, const float* __restrict__ part,
+    const void* __restrict__ w, int dt, int64_t n, int64_t k, const float* __restrict__ part,
     int nparts, uint8_t* __restrict__ codes, float* __restrict__ scale_out) {
   __shared__ float red[kWaves];
-  const float s = weight_scale(reduce_partials(part, nparts, red));
+  const float s = weight_scale(reduce_partials(part, nparts, red), dt);
   if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
   const int64_t total = n * k;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * kThreads)
-    codes[i] = weight_code(bf2f(w[i]), s, false);
+    codes[i] = weight_code(ld_elem(w, dt, i), s, false, dt);
 }
 
 // ---------------------------------------------------------------------------
@@ -474,6 +488,8 @@ int partial_blocks(int64_t rows) {
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool dtype_ok(int dt) { return dt == FVSR_DT_BF16 || dt == FVSR_DT_F16 || dt == FVSR_DT_F32; }
 
 // Compute units of the current device (persistent grids).
 int64_t cu_count() {
@@ -503,7 +519,8 @@ int launch_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uint8
   } else if (vec && vpl <= 18) {
     hipLaunchKernelGGL((quant_rows_vec<18, GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
   } else {
-    hipLaunchKernelGGL((quant_rows_generic<GELU>), grid, block, 0, st, x, rows, cols, ld, q, s);
+    hipLaunchKernelGGL((quant_rows_generic<GELU>), grid, block, 0, st, x, FVSR_DT_BF16, rows,
+                       cols, ld, q, s);
   }
   return fvsr_launch_status();
 }
@@ -517,9 +534,21 @@ void launch_gelu_tensor_codes(const uint16_t* x, int64_t rows, int64_t cols, int
     hipLaunchKernelGGL((quant_tensor_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0,
                        st, x, rows, cols, ld, part, P, q, s);
   } else {
-    hipLaunchKernelGGL((quant_tensor<true, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
-                       ld, part, P, q, s);
+    hipLaunchKernelGGL((quant_tensor<true, true>), dim3(P), dim3(kThreads), 0, st, x,
+                       FVSR_DT_BF16, rows, cols, ld, part, P, q, s);
   }
+}
+
+// Per-tensor quantisation by element loads of type dt (two launches).
+template <bool GELU>
+int launch_tensor_scalar(const void* x, int dt, int64_t rows, int64_t cols, int64_t ld,
+                         uint8_t* q, float* s, float* ws, hipStream_t st) {
+  const int P = partial_blocks(rows);
+  hipLaunchKernelGGL((amax_partial<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, dt, rows,
+                     cols, ld, ws);
+  hipLaunchKernelGGL((quant_tensor<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, dt, rows,
+                     cols, ld, ws, P, q, s);
+  return fvsr_launch_status();
 }
 
 template <bool GELU>
@@ -537,19 +566,16 @@ int launch_tensor(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld, uin
     hipLaunchKernelGGL((quant_tensor_gelu_table<18>), dim3((unsigned)g), dim3(kTabWaves * 64), 0,
                        st, x, rows, cols, ld, ws, (int)g, q, s);
   } else if (vec && GELU) {
-    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
-                       ld, ws);
+    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x,
+                       FVSR_DT_BF16, rows, cols, ld, ws);
     launch_gelu_tensor_codes(x, rows, cols, ld, ws, P, q, s, st);
   } else if (vec) {
-    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
-                       ld, ws);
-    hipLaunchKernelGGL((quant_tensor<GELU, true>), dim3(P), dim3(kThreads), 0, st, x, rows, cols,
-                       ld, ws, P, q, s);
+    hipLaunchKernelGGL((amax_partial<GELU, true>), dim3(P), dim3(kThreads), 0, st, x,
+                       FVSR_DT_BF16, rows, cols, ld, ws);
+    hipLaunchKernelGGL((quant_tensor<GELU, true>), dim3(P), dim3(kThreads), 0, st, x,
+                       FVSR_DT_BF16, rows, cols, ld, ws, P, q, s);
   } else {
-    hipLaunchKernelGGL((amax_partial<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, rows,
-                       cols, ld, ws);
-    hipLaunchKernelGGL((quant_tensor<GELU, false>), dim3(P), dim3(kThreads), 0, st, x, rows,
-                       cols, ld, ws, P, q, s);
+    return launch_tensor_scalar<GELU>(x, FVSR_DT_BF16, rows, cols, ld, q, s, ws, st);
   }
   return fvsr_launch_status();
 }
@@ -601,32 +627,70 @@ extern "C" int fvsr_gelu_quant_fp8_tensor(const void* h, int64_t rows, int64_t c
   if (vec)
     launch_gelu_tensor_codes(hp, rows, cols, cols, gpart, P, qp, scale_out, st);
   else
-    hipLaunchKernelGGL((quant_tensor<true, false>), dim3(P), dim3(kThreads), 0, st, hp, rows,
-                       cols, cols, gpart, P, qp, scale_out);
+    hipLaunchKernelGGL((quant_tensor<true, false>), dim3(P), dim3(kThreads), 0, st, hp,
+                       FVSR_DT_BF16, rows, cols, cols, gpart, P, qp, scale_out);
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_quant_weight_fp8_dt(const void* w, int w_dtype, int64_t n, int64_t k,
+                                        int mode, void* codes, float* scale_out,
+                                        float* workspace, int64_t workspace_floats,
+                                        void* stream) {
+  if (n < 0 || k < 0 || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW) ||
+      !dtype_ok(w_dtype))
+    return FVSR_EINVAL;
+  if (n == 0 || k == 0) return FVSR_OK;
+  if (!w || !codes || !scale_out) return FVSR_EINVAL;
+  hipStream_t st = (hipStream_t)stream;
+  uint8_t* qp = (uint8_t*)codes;
+  if (mode == FVSR_SCALE_ROW) {
+    hipLaunchKernelGGL(quant_weight_rows, dim3((unsigned)((n + kWaves - 1) / kWaves)),
+                       dim3(kThreads), 0, st, w, w_dtype, n, k, qp, scale_out);
+    return fvsr_launch_status();
+  }
+  const int P = partial_blocks(n);
+  if (!workspace || workspace_floats < P) return FVSR_EWORKSPACE;
+  hipLaunchKernelGGL((amax_partial<false, false>), dim3(P), dim3(kThreads), 0, st, w, w_dtype, n,
+                     k, k, workspace);
+  hipLaunchKernelGGL(quant_weight_tensor, dim3(P), dim3(kThreads), 0, st, w, w_dtype, n, k,
+                     workspace, P, qp, scale_out);
   return fvsr_launch_status();
 }
 
 extern "C" int fvsr_quant_weight_fp8(const void* w, int64_t n, int64_t k, int mode, void* codes,
                                      float* scale_out, float* workspace, int64_t workspace_floats,
                                      void* stream) {
-  if (n < 0 || k < 0 || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW)) return FVSR_EINVAL;
-  if (n == 0 || k == 0) return FVSR_OK;
-  if (!w || !codes || !scale_out) return FVSR_EINVAL;
+  return fvsr_quant_weight_fp8_dt(w, FVSR_DT_BF16, n, k, mode, codes, scale_out, workspace,
+                                  workspace_floats, stream);
+}
+
+extern "C" int fvsr_quant_fp8_dt(const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                 int64_t ld, int mode, int gelu, void* codes, float* scale_out,
+                                 float* workspace, int64_t workspace_floats, void* stream) {
+  if (!dtype_ok(x_dtype)) return FVSR_EINVAL;
+  if (x_dtype == FVSR_DT_BF16)
+    return fvsr_quant_fp8(x, rows, cols, ld, mode, gelu, codes, scale_out, workspace,
+                          workspace_floats, stream);
+  if (rows < 0 || cols < 0 || ld < cols || (mode != FVSR_SCALE_TENSOR && mode != FVSR_SCALE_ROW))
+    return FVSR_EINVAL;
+  if (rows == 0 || cols == 0) return FVSR_OK;
+  if (!x || !codes || !scale_out) return FVSR_EINVAL;
   hipStream_t st = (hipStream_t)stream;
-  const uint16_t* wp = (const uint16_t*)w;
   uint8_t* qp = (uint8_t*)codes;
   if (mode == FVSR_SCALE_ROW) {
-    hipLaunchKernelGGL(quant_weight_rows, dim3((unsigned)((n + kWaves - 1) / kWaves)),
-                       dim3(kThreads), 0, st, wp, n, k, qp, scale_out);
+    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves)), block(kThreads);
+    if (gelu)
+      hipLaunchKernelGGL((quant_rows_generic<true>), grid, block, 0, st, x, x_dtype, rows, cols,
+                         ld, qp, scale_out);
+    else
+      hipLaunchKernelGGL((quant_rows_generic<false>), grid, block, 0, st, x, x_dtype, rows, cols,
+                         ld, qp, scale_out);
     return fvsr_launch_status();
   }
-  const int P = partial_blocks(n);
-  if (!workspace || workspace_floats < P) return FVSR_EWORKSPACE;
-  hipLaunchKernelGGL((amax_partial<false, false>), dim3(P), dim3(kThreads), 0, st, wp, n, k, k,
-                     workspace);
-  hipLaunchKernelGGL(quant_weight_tensor, dim3(P), dim3(kThreads), 0, st, wp, n, k, workspace, P,
-                     qp, scale_out);
-  return fvsr_launch_status();
+  if (!workspace || workspace_floats < partial_blocks(rows)) return FVSR_EWORKSPACE;
+  return gelu ? launch_tensor_scalar<true>(x, x_dtype, rows, cols, ld, qp, scale_out, workspace, st)
+              : launch_tensor_scalar<false>(x, x_dtype, rows, cols, ld, qp, scale_out, workspace,
+                                            st);
 }
 
 // ---------------------------------------------------------------------------

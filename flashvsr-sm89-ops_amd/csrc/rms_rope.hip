@@ -138,38 +138,49 @@ __global__ __launch_bounds__(kThreads) void rms_rope_qkv_rows_vec(
     if (lane + 64 * j < nchunk) *(u32x4_t*)(out + (lane + 64 * j) * 8) = t[j];
 }
 
-// Any shape: scalar loads, partner element read directly.
+// Any shape and input types (x and w of types xt, wt; out of type xt): scalar
+// loads, partner element read directly.  Each lane sums the squares of its
+// 8-element chunks in order (then the last D % 8 elements), as rms_rope_row
+// does, so rows of bf16 values give that kernel's results bit for bit.
 __global__ __launch_bounds__(kThreads) void rms_rope_generic(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const float* __restrict__ cs,
-    uint16_t* __restrict__ out, int64_t rows, int64_t L, int64_t D, int64_t head_dim, float eps,
-    int rope) {
+    const void* __restrict__ x, int xt, const void* __restrict__ w, int wt,
+    const float* __restrict__ cs, void* __restrict__ out, int64_t rows, int64_t L, int64_t D,
+    int64_t head_dim, float eps, int rope) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const uint16_t* xr = x + row * D;
+  const int64_t xr = row * D;
   float sq = 0.0f;
-  for (int64_t d = lane; d < D; d += 64) {
-    const float a = bf2f(xr[d]);
+  for (int64_t c = lane; c < (D >> 3); c += 64) {
+    for (int e = 0; e < 8; ++e) {
+      const float a = ld_elem(x, xt, xr + c * 8 + e);
+      sq = __builtin_fmaf(a, a, sq);
+    }
+  }
+  for (int64_t d = (D & ~(int64_t)7) + lane; d < D; d += 64) {
+    const float a = ld_elem(x, xt, xr + d);
     sq = __builtin_fmaf(a, a, sq);
   }
   const float r = rsqrtf(wave_sum(sq) / (float)D + eps);
   const int64_t s = row % L;
   for (int64_t d = lane; d < D; d += 64) {
-    const float y = rbf16(bf2f(xr[d]) * r) * bf2f(w[d]);
+    const float y = rbf16(ld_elem(x, xt, xr + d) * r) * ld_elem(w, wt, d);
     float o = y;
     if (rope) {
       const int64_t dp = d ^ 1;
-      const float yp = rbf16(bf2f(xr[dp]) * r) * bf2f(w[dp]);
+      const float yp = rbf16(ld_elem(x, xt, xr + dp) * r) * ld_elem(w, wt, dp);
       const int64_t i = (d % head_dim) >> 1;
       const float cc = cs[(s * (head_dim >> 1) + i) * 2], ss = cs[(s * (head_dim >> 1) + i) * 2 + 1];
       // the same expressions as the vector kernel (ye, yo = even, odd)
       o = (d & 1) ? __builtin_fmaf(yp, ss, y * cc) : __builtin_fmaf(y, cc, -(yp * ss));
     }
-    out[row * D + d] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xffff);
+    st_elem(out, xt, xr + d, round_bf16(o));
   }
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+bool dtype_ok(int dt) { return dt == FVSR_DT_BF16 || dt == FVSR_DT_F16 || dt == FVSR_DT_F32; }
 
 }  // namespace
 
@@ -194,8 +205,25 @@ extern "C" int fvsr_rms_rope(const void* x, const void* weight, const float* cs,
     hipLaunchKernelGGL((rms_rope_vec<3, false>), grid, block, 0, st, xp, wp, cs, op, rows, L, D,
                        head_dim > 0 ? head_dim : D, eps);
   else
-    hipLaunchKernelGGL(rms_rope_generic, grid, block, 0, st, xp, wp, cs, op, rows, L, D,
-                       head_dim > 0 ? head_dim : D, eps, rope);
+    hipLaunchKernelGGL(rms_rope_generic, grid, block, 0, st, x, FVSR_DT_BF16, weight,
+                       FVSR_DT_BF16, cs, out, rows, L, D, head_dim > 0 ? head_dim : D, eps, rope);
+  return fvsr_launch_status();
+}
+
+extern "C" int fvsr_rms_rope_dt(const void* x, int x_dtype, const void* weight, int weight_dtype,
+                                const float* cs, void* out, int64_t B, int64_t L, int64_t D,
+                                int64_t head_dim, float eps, int rope, void* stream) {
+  if (!dtype_ok(x_dtype) || !dtype_ok(weight_dtype)) return FVSR_EINVAL;
+  if (x_dtype == FVSR_DT_BF16 && weight_dtype == FVSR_DT_BF16)
+    return fvsr_rms_rope(x, weight, cs, out, B, L, D, head_dim, eps, rope, stream);
+  if (B < 0 || L < 0 || D <= 0) return FVSR_EINVAL;
+  if (rope && (head_dim <= 0 || head_dim % 2 || D % head_dim || !cs)) return FVSR_EINVAL;
+  const int64_t rows = B * L;
+  if (rows == 0) return FVSR_OK;
+  if (!x || !weight || !out) return FVSR_EINVAL;
+  hipLaunchKernelGGL(rms_rope_generic, dim3((unsigned)((rows + kWaves - 1) / kWaves)),
+                     dim3(kThreads), 0, (hipStream_t)stream, x, x_dtype, weight, weight_dtype, cs,
+                     out, rows, L, D, head_dim > 0 ? head_dim : D, eps, rope);
   return fvsr_launch_status();
 }
 

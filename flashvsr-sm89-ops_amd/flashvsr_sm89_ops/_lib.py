@@ -19,6 +19,8 @@ LIB_PATH = os.environ.get("FVSR_LIB", os.path.join(_HERE, "libfvsr.so"))
 FVSR_OK, FVSR_EINVAL, FVSR_EHIP, FVSR_EUNSUPPORTED, FVSR_EWORKSPACE = 0, -1, -2, -3, -4
 SCALE_TENSOR, SCALE_ROW = 0, 1
 EPI_BIAS, EPI_ROWMAX, EPI_GATE_ADD = 0, 1, 2
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+_DT = {torch.bfloat16: DT_BF16, torch.float16: DT_F16, torch.float32: DT_F32}
 
 _ERR = {
     FVSR_EINVAL: "invalid argument",
@@ -39,6 +41,11 @@ _SIGS = {
     "fvsr_quant_fp8_noalloc": ([_P, _I64, _I64, _I64, _I, _I, _P, _P, _P], _I),
     "fvsr_gelu_quant_fp8_tensor": ([_P, _I64, _I64, _P, _I64, _P, _P, _P, _I64, _P], _I),
     "fvsr_quant_weight_fp8": ([_P, _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
+    "fvsr_quant_fp8_dt": ([_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P, _I64, _P], _I),
+    "fvsr_quant_weight_fp8_dt": ([_P, _I, _I64, _I64, _I, _P, _P, _P, _I64, _P], _I),
+    "fvsr_ln_modulate_dt": ([_P, _I, _P, _I, _P, _I, _P, _I64, _I64, _I64, _F, _P], _I),
+    "fvsr_gate_add_dt": ([_P, _I, _P, _I, _P, _I, _P, _I64, _I64, _I64, _P], _I),
+    "fvsr_rms_rope_dt": ([_P, _I, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _F, _I, _P], _I),
     "fvsr_fp8_gemm": ([_P, _I64, _P, _I, _P, _I64, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I,
                        _P, _P, _P, _P], _I),
     "fvsr_gemm_amax_parts": ([_I64], _I64),
@@ -125,6 +132,15 @@ def require_gpu(*ts):
 def require_dtype(t: torch.Tensor, dtype, name: str):
     if t.dtype != dtype:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def dtype_code(t: torch.Tensor, name: str) -> int:
+    """FVSR_DT_* code of a floating tensor of the *_dt entry points: bf16,
+    fp16 or fp32, the input types the reference's kernels load."""
+    code = _DT.get(t.dtype)
+    if code is None:
+        raise TypeError(f"{name} must be bfloat16, float16 or float32, got {t.dtype}")
+    return code
 
 
 def version() -> str:

@@ -23,29 +23,14 @@ import torch.nn as nn
 
 from . import _lib
 from .fp8_linear import FP8Linear, fp8_gemm, quantize_input_fp8
-from .fp8_quant import FP8_MAX, _workspace, quantize_fp8  # noqa: F401
+from .fp8_quant import FP8_MAX, quantize_fp8, quantize_rows_fp8  # noqa: F401
 
 
 def fused_gelu_quant_fp8(y2: torch.Tensor, per_token: bool = False):
-    """y2: [M, K] bf16 -> (e4m3 codes of gelu_tanh(y2), scale), the bf16 GELU
-    never materialised (fp8_ffn.py:57-72)."""
-    _lib.require_gpu(y2)
-    _lib.require_dtype(y2, torch.bfloat16, "y2")
-    M, K = y2.shape
-    if y2.numel() and y2.stride(1) != 1:
-        y2 = y2.contiguous()
-    x8 = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=y2.device)
-    alloc = torch.zeros if y2.numel() == 0 else torch.empty  # the kernels write every scale
-    s = alloc((M, 1) if per_token else (1,), dtype=torch.float32, device=y2.device)
-    if y2.numel() == 0:
-        return x8, s
-    mode = _lib.SCALE_ROW if per_token else _lib.SCALE_TENSOR
-    ws = None if per_token else _workspace(y2, M, K, mode)  # per-row scales need none
-    _lib.check(_lib.lib().fvsr_quant_fp8(y2.data_ptr(), M, K, y2.stride(0), mode, 1,
-                                         x8.data_ptr(), s.data_ptr(), _lib.ptr(ws),
-                                         0 if ws is None else ws.numel(), _lib.stream(y2)),
-               "fused_gelu_quant_fp8")
-    return x8, s
+    """y2: [M, K] bf16, fp16 or fp32 -> (e4m3 codes of bf16(gelu_tanh(y2)),
+    scale), the GELU never materialised (fp8_ffn.py:34-72: loaded as fp32,
+    GELU rounded to bf16, quantised as quantize_fp8)."""
+    return quantize_rows_fp8(y2, per_token, gelu=True, what="fused_gelu_quant_fp8")
 
 
 def gemm_gelu_quant_fp8(x8: torch.Tensor, s: torch.Tensor, lin, per_token: bool):

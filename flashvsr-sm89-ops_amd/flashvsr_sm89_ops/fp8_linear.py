@@ -9,6 +9,13 @@ The GEMM is the hand-written gfx950 kernel behind ``fvsr_fp8_gemm``.
 Scale granularity is per tensor by default, as in the reference.
 ``per_channel=True`` quantises the weight per output channel and
 ``per_token=True`` the activations per row (the BASELINE configurations).
+
+Weights and activations may be bf16, fp16 or fp32: the weight is quantised
+with eager's arithmetic in its own type (reference fp8_linear.py:19-22) and
+activations as the reference's quantisation kernel loads them (as fp32).  The
+output is bf16 (``out_dtype=torch.bfloat16`` there); a bias of another type
+is rounded to bf16 for the epilogue (torch._scaled_mm itself refuses a
+non-bf16 bias with a bf16 output).
 """
 from __future__ import annotations
 
@@ -112,15 +119,14 @@ def quantize_input_fp8(x2: torch.Tensor, per_token: bool = False):
     (reference fp8_linear.py:35-40, fp8_ffn.py:88-92).  A contiguous [M, K]
     goes through quantize_fp8.  For any other layout the reference evaluates
     ``s = (x2.abs().amax() / 448).clamp(min=1e-12).float()`` and
-    ``(x2 / s).to(e4m3)`` eagerly: bf16 tensors, so the scale and x/s are
-    each rounded to bf16 before the cast.  That is the expression of its
+    ``(x2 / s).to(e4m3)`` eagerly in x2's type, so the scale and x/s are each
+    rounded to that type before the cast.  That is the expression of its
     per-tensor weight quantisation, so those codes come from the same kernel
     (on a contiguous copy).  Per-token scales (this build's extension) read
     strided rows directly."""
     if per_token or x2.is_contiguous():
         return quantize_fp8(x2, per_token=per_token)
     _lib.require_gpu(x2)
-    _lib.require_dtype(x2, torch.bfloat16, "x2")
     return quantize_weight_fp8(x2.contiguous(), per_channel=False)
 
 
@@ -166,9 +172,6 @@ class FP8Linear(nn.Module):
         if linear is None:  # filled by from_quantized
             return
         w = linear.weight.detach()
-        if w.dtype != torch.bfloat16:
-            raise TypeError(f"FP8Linear quantises bf16 weights (the FlashVSR DiT's dtype); got "
-                            f"{w.dtype}. Cast the model to bfloat16 before converting.")
         q, s = quantize_weight_fp8(w, per_channel=per_channel)
         bias = linear.bias.detach().clone() if linear.bias is not None else None
         self._set(q, s, bias)

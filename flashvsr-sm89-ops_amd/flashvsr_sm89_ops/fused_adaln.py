@@ -1,4 +1,4 @@
-"""Fused AdaLN elementwise chains (bf16) on gfx950.
+"""Fused AdaLN elementwise chains on gfx950.
 
 `fused_ln_modulate(x, scale, shift)`: LayerNorm (no affine) then
 ``x*(1+scale)+shift`` with eager's per-op bf16 roundings
@@ -9,6 +9,11 @@ bitwise equal to eager (fused_adaln.py:45-57,74-85).
 `fused_ln_modulate_quant` additionally returns the per-row e4m3 codes of the
 modulated rows from the same pass (the activation quantisation of the FP8
 linear that consumes them).
+
+The two reference ops take x and the [B, 1, D] parameters in bf16, fp16 or
+fp32, each in its own type, and return x's type, as the reference's kernels
+(loads ``.to(tl.float32)``, output ``torch.empty_like(x)``); the fused
+extensions of this module take bf16.
 """
 from __future__ import annotations
 
@@ -17,28 +22,37 @@ import torch
 from . import _lib
 
 
-def _check_params(x, *ps):
+def _check_param_sizes(x, *ps):
+    """Every [B, 1, D] parameter holds B*D elements (the kernels read them all)."""
     B, L, D = x.shape
-    _lib.require_dtype(x, torch.bfloat16, "x")
     for p in ps:
-        _lib.require_dtype(p, torch.bfloat16, "modulation parameter")
         if p.numel() != B * D:
             raise ValueError(f"modulation parameter shape {tuple(p.shape)} does not match "
                              f"[B, 1, D] = [{B}, 1, {D}]")
 
 
+def _check_params(x, *ps):
+    """The fused extensions' operands: bf16 x and bf16 [B, 1, D] parameters."""
+    _lib.require_dtype(x, torch.bfloat16, "x")
+    for p in ps:
+        _lib.require_dtype(p, torch.bfloat16, "modulation parameter")
+    _check_param_sizes(x, *ps)
+
+
 def fused_ln_modulate(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor,
                       eps: float = 1e-6):
-    """LayerNorm(affine=False) + modulate. x [B, L, D] contiguous bf16;
-    scale/shift [B, 1, D]."""
+    """LayerNorm(affine=False) + modulate. x [B, L, D] contiguous; scale/shift
+    [B, 1, D]; each bf16, fp16 or fp32.  Returns x's type."""
     B, L, D = x.shape
     assert x.is_contiguous() and scale.is_contiguous() and shift.is_contiguous()
     _lib.require_gpu(x, scale, shift)
-    _check_params(x, scale, shift)
+    dts = (_lib.dtype_code(x, "x"), _lib.dtype_code(scale, "scale"),
+           _lib.dtype_code(shift, "shift"))
+    _check_param_sizes(x, scale, shift)
     out = torch.empty_like(x)
-    _lib.check(_lib.lib().fvsr_ln_modulate(x.data_ptr(), scale.data_ptr(), shift.data_ptr(),
-                                           out.data_ptr(), B, L, D, float(eps), None, None,
-                                           _lib.stream(x)), "fused_ln_modulate")
+    _lib.check(_lib.lib().fvsr_ln_modulate_dt(x.data_ptr(), dts[0], scale.data_ptr(), dts[1],
+                                              shift.data_ptr(), dts[2], out.data_ptr(), B, L, D,
+                                              float(eps), _lib.stream(x)), "fused_ln_modulate")
     return out
 
 
@@ -61,19 +75,21 @@ def fused_ln_modulate_quant(x: torch.Tensor, scale: torch.Tensor, shift: torch.T
 
 
 def fused_gate_add(x: torch.Tensor, gate: torch.Tensor, residual: torch.Tensor):
-    """x + gate * residual. x/residual [B, L, D] contiguous bf16; gate [B, 1, D]."""
+    """x + gate * residual. x/residual [B, L, D] contiguous; gate [B, 1, D];
+    each bf16, fp16 or fp32.  Returns x's type."""
     B, L, D = x.shape
     assert x.is_contiguous() and residual.is_contiguous() and gate.is_contiguous()
     if residual.shape != x.shape:
         raise ValueError(f"fused_gate_add: residual {tuple(residual.shape)} does not match x "
                          f"{tuple(x.shape)}")
     _lib.require_gpu(x, gate, residual)
-    _lib.require_dtype(residual, torch.bfloat16, "residual")
-    _check_params(x, gate)
+    dts = (_lib.dtype_code(x, "x"), _lib.dtype_code(gate, "gate"),
+           _lib.dtype_code(residual, "residual"))
+    _check_param_sizes(x, gate)
     out = torch.empty_like(x)
-    _lib.check(_lib.lib().fvsr_gate_add(x.data_ptr(), gate.data_ptr(), residual.data_ptr(),
-                                        out.data_ptr(), B, L, D, _lib.stream(x)),
-               "fused_gate_add")
+    _lib.check(_lib.lib().fvsr_gate_add_dt(x.data_ptr(), dts[0], gate.data_ptr(), dts[1],
+                                           residual.data_ptr(), dts[2], out.data_ptr(), B, L, D,
+                                           _lib.stream(x)), "fused_gate_add")
     return out
 
 

@@ -1,4 +1,4 @@
-"""Fused RMSNorm + RoPE (bf16) on gfx950.
+"""Fused RMSNorm + RoPE on gfx950.
 
 Same contract as the reference (flashvsr_sm89_ops/fused_rms_rope.py:21-83):
 RMS over the full hidden dim D in fp32, ``y = bf16(x*rsqrt(ms+eps)) * w``,
@@ -9,6 +9,11 @@ The kernel reads (cos, sin) in the interleaved layout of
 ``view_as_real(freqs_cis)`` (fp32 [S, head_dim/2, 2]), so a complex64
 freqs_cis is used without any copy; other dtypes are converted once and
 cached per freqs tensor.
+
+`fused_rms_rope` takes x and the weight in bf16, fp16 or fp32, each in its
+own type, and returns x's type, as the reference's kernel (loads
+``.to(tl.float32)``, output ``torch.empty_like(x)``); the fused q/k forms of
+this module take bf16.
 """
 from __future__ import annotations
 
@@ -77,18 +82,19 @@ def _check_weights(D: int, *weights):
 
 def fused_rms_rope(x: torch.Tensor, weight: torch.Tensor, freqs_cis, eps: float = 1e-6,
                    rope: bool = True, head_dim: int = 128):
-    """x [B, L, D] bf16 -> RMSNorm(weight) -> [x RoPE] (fused_rms_rope.py:66-83)."""
+    """x [B, L, D] -> RMSNorm(weight) -> [x RoPE] (fused_rms_rope.py:66-83);
+    x and weight bf16, fp16 or fp32; returns x's type."""
     B, L, D = x.shape
     _check_weights(D, weight)
     _lib.require_gpu(x, weight)
-    _lib.require_dtype(x, torch.bfloat16, "x")
+    xt, wt = _lib.dtype_code(x, "x"), _lib.dtype_code(weight, "weight")
     x2 = x.contiguous()
-    w = weight.to(torch.bfloat16).contiguous()
+    w = weight.contiguous()
     out = torch.empty_like(x2)
     cs = _table_for(freqs_cis, L, head_dim, x.device) if rope else None
-    _lib.check(_lib.lib().fvsr_rms_rope(x2.data_ptr(), w.data_ptr(), _lib.ptr(cs),
-                                        out.data_ptr(), B, L, D, head_dim if rope else D,
-                                        float(eps), int(bool(rope)), _lib.stream(x)),
+    _lib.check(_lib.lib().fvsr_rms_rope_dt(x2.data_ptr(), xt, w.data_ptr(), wt, _lib.ptr(cs),
+                                           out.data_ptr(), B, L, D, head_dim if rope else D,
+                                           float(eps), int(bool(rope)), _lib.stream(x)),
                "fused_rms_rope")
     return out
 

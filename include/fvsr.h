@@ -44,6 +44,9 @@ typedef enum {
 /* Granularity of an activation or weight scale. */
 enum { FVSR_SCALE_TENSOR = 0, FVSR_SCALE_ROW = 1 };
 
+/* Element types of the *_dt entry points' floating-point tensors. */
+enum { FVSR_DT_BF16 = 0, FVSR_DT_F16 = 1, FVSR_DT_F32 = 2 };
+
 /* GEMM epilogues. */
 enum {
   FVSR_EPI_BIAS = 0,     /* C = bf16(acc*sa*sb + bias)                                  */
@@ -200,6 +203,53 @@ int fvsr_gate_add(const void* x, const void* gate, const void* res, void* out, i
  */
 int fvsr_rms_rope(const void* x, const void* weight, const float* cs, void* out, int64_t B,
                   int64_t L, int64_t D, int64_t head_dim, float eps, int rope, void* stream);
+
+/*
+ * fp16 and fp32 inputs.  The reference's kernels load every floating input
+ * with .to(tl.float32) and store into torch.empty_like(x), so its ops take
+ * bf16, fp16 or fp32 tensors, each in its own type (fp8_quant.py:20,33;
+ * fused_adaln.py:29,37-38,53-55; fused_rms_rope.py:33,36,44).  These entry
+ * points take one FVSR_DT_* code per floating tensor; the arithmetic,
+ * including the bf16 roundings the reference makes, is that of the bf16
+ * entry points above, and outputs (except codes and scales) are written in
+ * x's type: a bf16-rounded result stored exactly in bf16 or fp32 and rounded
+ * to nearest even in fp16.  With every tensor bf16 they run the bf16 entry
+ * point's kernels.
+ */
+
+/* fvsr_quant_fp8 (fp8_quant.py:16-55, fp8_ffn.py:34-72) on x of type x_dtype;
+ * fp16/fp32 codes are those of the IEEE quotient x / s.  Same workspace. */
+int fvsr_quant_fp8_dt(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld,
+                      int mode, int gelu, void* codes, float* scale_out, float* workspace,
+                      int64_t workspace_floats, void* stream);
+
+/* fvsr_quant_weight_fp8 (fp8_linear.py:17-22) on a weight of type w_dtype,
+ * with eager's arithmetic in that type: w_scale = fp32(t((amax * fl(1/448)))
+ * clamped below at t(1e-12)) and codes e4m3(t(w / w_scale)), t() rounding to
+ * w_dtype (the GPU evaluates amax / 448 as a product with the reciprocal;
+ * t(1e-12) is 0 in fp16).  FVSR_SCALE_ROW: codes e4m3(w / s_n) in fp32.
+ * Codes follow torch's e4m3fn cast (NaN and |v| > 464 give 0x7F | sign). */
+int fvsr_quant_weight_fp8_dt(const void* w, int w_dtype, int64_t n, int64_t k, int mode,
+                             void* codes, float* scale_out, float* workspace,
+                             int64_t workspace_floats, void* stream);
+
+/* fvsr_ln_modulate's out-only form (fused_adaln.py:22-42,60-71) on x, scale
+ * and shift of any of the three types; out [B, L, D] has x's type. */
+int fvsr_ln_modulate_dt(const void* x, int x_dtype, const void* scale, int scale_dtype,
+                        const void* shift, int shift_dtype, void* out, int64_t B, int64_t L,
+                        int64_t D, float eps, void* stream);
+
+/* fvsr_gate_add (fused_adaln.py:45-57,74-85) on x, gate and res of any of the
+ * three types; out [B, L, D] has x's type. */
+int fvsr_gate_add_dt(const void* x, int x_dtype, const void* gate, int gate_dtype,
+                     const void* res, int res_dtype, void* out, int64_t B, int64_t L, int64_t D,
+                     void* stream);
+
+/* fvsr_rms_rope (fused_rms_rope.py:21-83) on x and weight of any of the three
+ * types; out [B, L, D] has x's type.  D and head_dim even. */
+int fvsr_rms_rope_dt(const void* x, int x_dtype, const void* weight, int weight_dtype,
+                     const float* cs, void* out, int64_t B, int64_t L, int64_t D,
+                     int64_t head_dim, float eps, int rope, void* stream);
 
 /* Both self-attention projections in one launch (q and k share the cos/sin
  * reads): the two fused_rms_rope calls of integrate.py:59-62.  Rows of q/k

@@ -31,6 +31,14 @@
  *   orc_quant_weight  contract Q-W: per-tensor (fp8_linear.py:17-22, with the
  *                     bf16 intermediate roundings of eager type promotion) and
  *                     per-output-channel (fp32 division, single rounding).
+ *   orc_quant_rows_f32, orc_quant_weight_f32
+ *                     the same contracts on fp16 or fp32 inputs (given as
+ *                     their exact fp32 values): the reference's kernels load
+ *                     any floating input as fp32 (fp8_quant.py:20,33), and
+ *                     FP8Linear's eager weight expressions run in the weight's
+ *                     own type (fp8_linear.py:19-22).
+ *   orc_f16_round     fp32 -> IEEE binary16, round to nearest even (subnormals,
+ *                     overflow to inf), returned as fp32.
  */
 #include <math.h>
 #include <stdint.h>
@@ -48,6 +56,28 @@ static inline float bf16r(float f) {
 }
 static inline float bf2f(uint16_t h) { return u2f((uint32_t)h << 16); }
 static inline uint16_t f2bf(float f) { return (uint16_t)(f2u(bf16r(f)) >> 16); }
+
+/* binary16 round-to-nearest-even of an fp32 value, returned as fp32.  Normal
+ * range: 10 mantissa bits kept by the add-and-mask rounding; below 2^-14 the
+ * grid is 2^-24 (subnormals); 65520 and above round to infinity. */
+static float f16r(float f) {
+    uint32_t u = f2u(f), sign = u & 0x80000000u, a = u & 0x7fffffffu;
+    if (a > 0x7f800000u) return f;                       /* NaN */
+    if (a >= 0x477ff000u) return u2f(sign | 0x7f800000u);
+    if (a < 0x38800000u) {
+        float m = nearbyintf(u2f(a) * 16777216.0f);      /* exact scale by 2^24, RNE */
+        return u2f(sign | f2u(m / 16777216.0f));          /* exact */
+    }
+    a += 0xfffu + ((a >> 13) & 1u);
+    return u2f(sign | (a & 0xffffe000u));
+}
+
+void orc_f16_round(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = f16r(x[i]);
+}
+
+/* Element type of the float-input entry points: 0 bf16, 1 fp16, 2 fp32. */
+static float round_dt(float v, int dt) { return dt == 2 ? v : (dt == 1 ? f16r(v) : bf16r(v)); }
 
 uint8_t orc_e4m3_one(float f) {
     uint32_t u = f2u(f);
@@ -126,11 +156,21 @@ void orc_gelu_bf16(const uint16_t* h, uint16_t* g, int64_t n) {
     for (int64_t i = 0; i < n; ++i) g[i] = f2bf(orc_gelu_one(bf2f(h[i])));
 }
 
-/* Q-A over a [rows, cols] bf16 matrix (leading dimension ld elements).
+/* The same GELU on fp32 inputs (bf16-rounded results as fp32). */
+void orc_gelu_f32(const float* x, float* g, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) g[i] = orc_gelu_one(x[i]);
+}
+
+/* Element i of x: bf16 bits (f32 = 0) or fp32 values (f32 = 1). */
+static float ld_x(const void* x, int f32, int64_t i) {
+    return f32 ? ((const float*)x)[i] : bf2f(((const uint16_t*)x)[i]);
+}
+
+/* Q-A over a [rows, cols] matrix (leading dimension ld elements).
  * per_row = 0: one scale for the whole matrix (scale[0]); per_row = 1: one per row.
  * gelu = 1 quantises gelu(x) instead of x (fp8_ffn.py:43-54). */
-void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
-                    int per_row, int gelu, uint8_t* q, float* scale_out) {
+static void quant_rows(const void* x, int f32, int64_t rows, int64_t cols, int64_t ld,
+                       int per_row, int gelu, uint8_t* q, float* scale_out) {
     const float FP8_MAX = 448.0f;
     int64_t groups = per_row ? rows : 1;
     int64_t rpg = per_row ? 1 : rows;
@@ -138,7 +178,7 @@ void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
         float amax = 0.0f;
         for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
             for (int64_t c = 0; c < cols; ++c) {
-                float v = bf2f(x[r * ld + c]);
+                float v = ld_x(x, f32, r * ld + c);
                 if (gelu) v = orc_gelu_one(v);
                 v = fabsf(v);
                 if (v > amax) amax = v;
@@ -146,7 +186,7 @@ void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
         float s = (amax > 1e-12f ? amax : 1e-12f) / FP8_MAX;
         for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
             for (int64_t c = 0; c < cols; ++c) {
-                float v = bf2f(x[r * ld + c]);
+                float v = ld_x(x, f32, r * ld + c);
                 if (gelu) v = orc_gelu_one(v);
                 v = v / s;
                 v = v < -FP8_MAX ? -FP8_MAX : v;
@@ -155,6 +195,17 @@ void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
             }
         scale_out[g] = amax * (1.0f / FP8_MAX);
     }
+}
+
+void orc_quant_rows(const uint16_t* x, int64_t rows, int64_t cols, int64_t ld,
+                    int per_row, int gelu, uint8_t* q, float* scale_out) {
+    quant_rows(x, 0, rows, cols, ld, per_row, gelu, q, scale_out);
+}
+
+/* Q-A on fp16 or fp32 inputs given as fp32 values. */
+void orc_quant_rows_f32(const float* x, int64_t rows, int64_t cols, int64_t ld,
+                        int per_row, int gelu, uint8_t* q, float* scale_out) {
+    quant_rows(x, 1, rows, cols, ld, per_row, gelu, q, scale_out);
 }
 
 /* Q-W.  per_channel = 0 (fp8_linear.py:20-22):
@@ -180,6 +231,39 @@ void orc_quant_weight(const uint16_t* w, int64_t n, int64_t k, int per_channel,
             for (int64_t c = 0; c < k; ++c) {
                 float v = bf2f(w[r * k + c]) / s;
                 if (!per_channel) v = bf16r(v);
+                q[r * k + c] = orc_e4m3_one(v);
+            }
+        scale_out[g] = s;
+    }
+}
+
+/* Q-W on a weight of type dt (0 bf16, 1 fp16, 2 fp32) given as fp32 values,
+ * with eager torch's arithmetic in that type on the GPU:
+ *   w_scale = fp32(t(amax * fl(1/448)) clamped below at t(1e-12))
+ *     (a tensor divided by a Python float is multiplied by the float
+ *     reciprocal there; the clamp compares in fp32 and its bound, rounded to
+ *     t, is 0 in fp16; t() rounds to dt)
+ *   per tensor:  q = e4m3(t(w / w_scale))   (a 0-dim fp32 scale does not
+ *                promote w, so the quotient is rounded to dt)
+ *   per channel: q = e4m3(w / s_n)          ([N, 1] fp32 scales promote it) */
+void orc_quant_weight_f32(const float* w, int64_t n, int64_t k, int per_channel, int dt,
+                          uint8_t* q, float* scale_out) {
+    const float lo = round_dt(1e-12f, dt);
+    int64_t groups = per_channel ? n : 1;
+    int64_t rpg = per_channel ? 1 : n;
+    for (int64_t g = 0; g < groups; ++g) {
+        float amax = 0.0f;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < k; ++c) {
+                float v = fabsf(w[r * k + c]);
+                if (v > amax) amax = v;
+            }
+        float s = round_dt(amax * (1.0f / 448.0f), dt);
+        if (s < lo) s = lo;
+        for (int64_t r = g * rpg; r < (g + 1) * rpg; ++r)
+            for (int64_t c = 0; c < k; ++c) {
+                float v = w[r * k + c] / s;
+                if (!per_channel) v = round_dt(v, dt);
                 q[r * k + c] = orc_e4m3_one(v);
             }
         scale_out[g] = s;

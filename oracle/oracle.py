@@ -47,6 +47,10 @@ def lib():
         L.orc_gelu_bf16.argtypes = [P, P, I64]
         L.orc_quant_rows.argtypes = [P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P, P]
         L.orc_quant_weight.argtypes = [P, I64, I64, ctypes.c_int, P, P]
+        L.orc_quant_rows_f32.argtypes = [P, I64, I64, I64, ctypes.c_int, ctypes.c_int, P, P]
+        L.orc_quant_weight_f32.argtypes = [P, I64, I64, ctypes.c_int, ctypes.c_int, P, P]
+        L.orc_f16_round.argtypes = [P, P, I64]
+        L.orc_gelu_f32.argtypes = [P, P, I64]
         L.orc_expf.argtypes = [ctypes.c_float]
         L.orc_expf.restype = ctypes.c_float
         _lib = L
@@ -128,6 +132,49 @@ def quantize_weight(w_bits: np.ndarray, per_channel: bool = False):
     s = np.empty(N if per_channel else 1, np.float32)
     lib().orc_quant_weight(_p(w_bits), N, K, int(per_channel), _p(q), _p(s))
     return q, s
+
+
+def f16(x) -> np.ndarray:
+    """Round float32 values to IEEE binary16 (nearest even), returned as float32."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().orc_f16_round(_p(x), _p(y), x.size)
+    return y
+
+
+DT_BF16, DT_F16, DT_F32 = 0, 1, 2
+
+
+def quantize_fp8_values(x: np.ndarray, per_row: bool = False, gelu: bool = False):
+    """Q-A as quantize_fp8 on fp16 or fp32 inputs, given as their float32
+    values (the reference's kernels load any input as fp32, fp8_quant.py:20,33)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    M, K = x.shape
+    q = np.empty((M, K), np.uint8)
+    s = np.empty(M if per_row else 1, np.float32)
+    lib().orc_quant_rows_f32(_p(x), M, K, K, int(per_row), int(gelu), _p(q), _p(s))
+    return q, s
+
+
+def quantize_weight_values(w: np.ndarray, dt: int, per_channel: bool = False):
+    """Q-W on a weight of type dt (DT_BF16 / DT_F16 / DT_F32) given as its
+    float32 values: fp8_linear.py:19-22 evaluated in that type (see
+    orc_quant_weight_f32).  Returns (codes uint8 [N,K], scale float32 [1] or [N])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    q = np.empty((N, K), np.uint8)
+    s = np.empty(N if per_channel else 1, np.float32)
+    lib().orc_quant_weight_f32(_p(w), N, K, int(per_channel), int(dt), _p(q), _p(s))
+    return q, s
+
+
+def gelu_values(x: np.ndarray) -> np.ndarray:
+    """bf16(tanh-GELU(x)) for float32 inputs, as float32 (the same sequence as
+    gelu_bf16; fp8_ffn.py:24-30 rounds to bf16 whatever the input type)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    g = np.empty_like(x)
+    lib().orc_gelu_f32(_p(x), _p(g), x.size)
+    return g
 
 
 def gelu_bf16(h_bits: np.ndarray) -> np.ndarray:

@@ -137,7 +137,12 @@ def test_fp8_ffn_forward_vs_oracle(monkeypatch, per_token, strided):
     assert bad.mean() <= 1e-3, f"FP8FFN chain: {bad.mean():.2e} beyond 2e-2, max {err.max():.3g}"
 
 
-def test_fp8_linear_rejects_non_bf16_weights():
+def test_fp8_linear_weight_types():
+    """fp32 and fp16 Linears convert (their weights are quantised in their own
+    type, covered in test_gpu_dtypes.py); any other type is refused."""
     from flashvsr_sm89_ops import FP8Linear
-    with pytest.raises(TypeError, match="bf16"):
-        FP8Linear(torch.nn.Linear(16, 16).to(DEV))
+    for dt in (torch.float32, torch.float16):
+        m = FP8Linear(torch.nn.Linear(16, 16).to(dt).to(DEV))
+        assert m.weight.dtype == torch.float8_e4m3fn and m.w_scale.dtype == torch.float32
+    with pytest.raises(TypeError, match="bfloat16, float16 or float32"):
+        FP8Linear(torch.nn.Linear(16, 16).double().to(DEV))

@@ -79,6 +79,33 @@ def test_argument_checks_before_launch(L):
     assert L.fvsr_block_index(None, 0, 4, 4, None, None, None) == _lib.FVSR_OK
 
 
+def test_dtype_entry_points_check_codes(L):
+    """The *_dt entry points take FVSR_DT_* codes (bf16 0, fp16 1, fp32 2) and
+    refuse any other before launching; empty calls return at once; the
+    wrappers map torch dtypes to codes and refuse other types."""
+    from flashvsr_sm89_ops import _lib
+    p = ctypes.c_void_p(16)  # never dereferenced
+    E, OK = _lib.FVSR_EINVAL, _lib.FVSR_OK
+    assert L.fvsr_gate_add_dt(p, 3, p, 0, p, 0, p, 1, 4, 8, None) == E
+    assert L.fvsr_gate_add_dt(p, 0, p, 0, p, -1, p, 1, 4, 8, None) == E
+    assert L.fvsr_ln_modulate_dt(p, 0, p, -1, p, 0, p, 1, 4, 8, 1e-6, None) == E
+    assert L.fvsr_ln_modulate_dt(p, 1, p, 2, p, 2, p, 1, 4, 0, 1e-6, None) == E   # D = 0
+    assert L.fvsr_rms_rope_dt(p, 0, p, 5, None, p, 1, 4, 8, 8, 1e-6, 0, None) == E
+    assert L.fvsr_rms_rope_dt(p, 2, p, 2, None, p, 1, 4, 8, 8, 1e-6, 1, None) == E  # rope, no cs
+    assert L.fvsr_quant_fp8_dt(p, 9, 4, 8, 8, 1, 0, p, p, None, 0, None) == E
+    assert L.fvsr_quant_fp8_dt(p, 2, 4, 8, 8, 0, 0, p, p, p, 0, None) == _lib.FVSR_EWORKSPACE
+    assert L.fvsr_quant_weight_fp8_dt(p, 9, 4, 8, 1, p, p, None, 0, None) == E
+    assert L.fvsr_gate_add_dt(None, 2, None, 1, None, 2, None, 0, 4, 8, None) == OK
+    assert L.fvsr_quant_fp8_dt(None, 1, 0, 8, 8, 1, 0, None, None, None, 0, None) == OK
+    assert L.fvsr_quant_weight_fp8_dt(None, 2, 0, 8, 0, None, None, None, 0, None) == OK
+    for dt, code in ((torch.bfloat16, 0), (torch.float16, 1), (torch.float32, 2)):
+        assert _lib.dtype_code(torch.zeros(1, dtype=dt), "x") == code == getattr(
+            _lib, {0: "DT_BF16", 1: "DT_F16", 2: "DT_F32"}[code])
+    for dt in (torch.float64, torch.int32, torch.float8_e4m3fn):
+        with pytest.raises(TypeError, match="bfloat16, float16 or float32"):
+            _lib.dtype_code(torch.zeros(1).to(dt), "x")
+
+
 def test_no_cpu_fallback():
     import flashvsr_sm89_ops as f
     x = torch.zeros(4, 16, dtype=torch.bfloat16)

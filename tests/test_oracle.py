@@ -159,6 +159,138 @@ def test_weight_quant_golden():
     assert np.array_equal(s, GOLD["wq_channel_s"])
 
 
+def test_f16_round_matches_numpy():
+    """O.f16 (binary16 round-to-nearest-even) against numpy's float16 cast:
+    every fp16 value, the fp32 values one ulp either side of every midpoint
+    between neighbours (the ties themselves included), the overflow boundary
+    and random fp32 bit patterns (subnormals, NaN, inf)."""
+    h = np.arange(0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)  # finite, >= 0
+    mid = ((h[:-1].astype(np.float64) + h[1:]) / 2).astype(np.float32)
+    up = np.nextafter(mid, np.float32(np.inf))
+    dn = np.nextafter(mid, np.float32(-np.inf))
+    edge = np.float32([65504, 65519.99, 65520, 65536, 1e9, 2.0 ** -25, 2.0 ** -24 * 1.5,
+                       np.inf, np.nan])
+    rnd = np.random.default_rng(7).integers(0, 2 ** 32, 200000, dtype=np.uint64) \
+        .astype(np.uint32).view(np.float32)
+    x = np.concatenate([h, mid, up, dn, edge, rnd])
+    x = np.concatenate([x, -x])
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).astype(np.float32)
+    got = O.f16(x)
+    assert np.array_equal(got, ref, equal_nan=True)
+
+
+def test_scale_over_448_reciprocal_rounds_like_division():
+    """amax / 448 in bf16 or fp16 (FP8Linear's weight scale): torch on the GPU
+    multiplies by fl(1/448) in fp32 and rounds to the 16-bit type.  For every
+    finite bf16 amax, and every fp16 amax whose quotient is a normal fp16, that
+    equals rounding the IEEE quotient (1/7 is periodic in binary, so neither
+    form lands near a tie).  Below fp16's normal range the quotient can sit
+    exactly on a tie of the subnormal grid, where the product's one-ulp error
+    decides the rounding; the oracle and the kernels form the product, as the
+    GPU does.  In fp32 the two forms differ for about half of all inputs."""
+    inv = np.float32(1.0) / np.float32(448.0)
+    b = (np.arange(0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    assert np.array_equal(O.bf16(b * inv), O.bf16(b / np.float32(448.0)))
+    h = np.arange(0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    diff = O.f16(h * inv) != O.f16(h / np.float32(448.0))
+    q = h[diff].astype(np.float64) / 448
+    assert (q < 2.0 ** -14).all()                        # subnormal results only
+    assert np.array_equal(q * 2.0 ** 24 % 1, np.full(q.size, 0.5))  # exact grid ties
+    assert 0 < diff.sum() < 64
+    assert (b * inv != b / np.float32(448.0)).mean() > 0.4
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_weight_quant_fp16_vs_torch_eager(per_channel):
+    """fp16 weights: the oracle against FP8Linear.__init__'s expressions
+    (fp8_linear.py:20-22) run by torch on fp16 tensors (CPU and GPU round the
+    16-bit scale the same way, checked above), including an all-zero weight,
+    whose scale is 0 in fp16 (1e-12 rounds to 0) and whose codes are NaN."""
+    g = torch.Generator().manual_seed(4)
+    for scale in (0.02, 30.0, 0.0):
+        w = (torch.randn(40, 96, generator=g) * scale).to(torch.float16)
+        w[3, 5] = 1e-7 if scale else 0.0                  # an fp16 subnormal
+        if per_channel:
+            s = (w.abs().amax(dim=1, keepdim=True) / 448.0).clamp(min=1e-12).float()
+        else:
+            s = (w.abs().amax() / 448.0).clamp(min=1e-12).float()
+        ref = (w / s).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        q, so = O.quantize_weight_values(w.float().numpy(), O.DT_F16, per_channel=per_channel)
+        assert np.array_equal(so, s.reshape(-1).numpy())
+        nan = (ref & 0x7F) == 0x7F
+        assert np.array_equal(q[~nan], ref[~nan]) and ((q[nan] & 0x7F) == 0x7F).all()
+        assert nan.all() == (scale == 0.0)
+
+
+def test_weight_quant_fp32_and_bf16_forms():
+    """fp32 weights: the per-tensor expression with the GPU's reciprocal
+    multiply written out (torch CPU would divide), codes from torch's cast of
+    the fp32 quotient; bf16-valued weights given as floats reproduce the bf16
+    oracle (whose scale divides: equal by the check above)."""
+    g = torch.Generator().manual_seed(5)
+    w = torch.randn(64, 80, generator=g) * 0.05
+    s = (w.abs().amax() * torch.tensor(1.0 / 448.0)).clamp(min=1e-12)
+    ref = (w / s).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    q, so = O.quantize_weight_values(w.numpy(), O.DT_F32)
+    assert so[0] == s.item() and np.array_equal(q, ref)
+    wb = O.bf16_bits(w.numpy())
+    for pc in (False, True):
+        q1, s1 = O.quantize_weight(wb, per_channel=pc)
+        q2, s2 = O.quantize_weight_values(O.from_bf16_bits(wb), O.DT_BF16, per_channel=pc)
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_quant_values_vs_torch_eager(per_row):
+    """Activation quantisation of fp32 and fp16 inputs against the reference's
+    formula in torch (fp8_quant.py:26-35,54: IEEE quotient, clamp, e4m3 cast;
+    returned scale amax * fl(1/448)), and bf16 values given as floats against
+    the bf16 oracle."""
+    g = torch.Generator().manual_seed(6)
+    for dt in (torch.float32, torch.float16):
+        x = (torch.randn(24, 520, generator=g) * 7).to(dt).float()
+        x[2] = 0
+        amax = x.abs().amax(dim=1, keepdim=True) if per_row else x.abs().amax()
+        s = amax.clamp(min=1e-12) / 448.0
+        ref = (x / s).clamp(-448, 448).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        q, so = O.quantize_fp8_values(x.numpy(), per_row=per_row)
+        assert np.array_equal(q, ref)
+        assert np.array_equal(so, (amax * torch.tensor(1.0 / 448.0)).reshape(-1).numpy())
+    xb = O.bf16_bits(np.random.default_rng(3).standard_normal((9, 77)).astype(np.float32))
+    for gelu in (False, True):
+        q1, s1 = O.quantize_fp8(xb, per_row=per_row, gelu=gelu)
+        q2, s2 = O.quantize_fp8_values(O.from_bf16_bits(xb), per_row=per_row, gelu=gelu)
+        assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+
+
+def test_gelu_on_fp32_inputs_vs_torch():
+    """The GELU of the requantisation on fp32 inputs (the reference's kernel
+    rounds it to bf16 whatever the input type, fp8_ffn.py:24-30): equal to the
+    reference's 1 - 2/(exp(2u)+1) form evaluated in numpy float32 with a
+    float64 exp (the formula pin), and to torch's fp32 tanh-GELU rounded to
+    bf16 outside the band where that identity cancels (x in [-5.2, -3.3]),
+    but for one-step moves next to a bf16 rounding boundary."""
+    x = np.random.default_rng(8).standard_normal(100000).astype(np.float32) * 4
+    x[:4] = [1e30, -1e30, 0.0, -0.0]
+    got = O.gelu_values(x)
+    f = np.float32
+    with np.errstate(over="ignore", invalid="ignore"):
+        u = f(0.7978845608028654) * (x + ((f(0.044715) * x) * x) * x)
+        e = np.exp((f(2.0) * u).astype(np.float64)).astype(np.float32)
+        g = O.bf16((f(0.5) * x) * (f(1.0) + (f(1.0) - f(2.0) / (e + f(1.0)))))
+    fin = np.isfinite(g)
+    assert (got[fin] == g[fin]).mean() > 0.999
+    assert got[0] == O.bf16(np.float32([1e30]))[0] and got[1] == 0 and got[2] == 0
+    ref = F.gelu(torch.from_numpy(x), approximate="tanh").to(torch.bfloat16).float().numpy()
+    out = (x < -5.2) | (x > -3.3)
+    same = got[out] == ref[out]
+    assert same.mean() > 0.999
+    a, b = got[out][~same], ref[out][~same]
+    assert (np.abs(a - b) <= np.abs(b) * 2.0 ** -7).all()
+    assert np.abs(got - ref).max() < 1e-3
+
+
 def test_gelu_quant_vs_unfused_torch_chain():
     """Codes equal the torch chain quantize(F.gelu(h)) except at elements
     whose GELU value differs (the cancellation band), which move by <= 1 code."""
