@@ -12,8 +12,10 @@ What differs from the reference package at its public surface:
   ``tile_weight``) are not part of this build: they drive the pipeline over
   spatial tiles and call none of these ops, so they stay with the reference;
   ``from flashvsr_sm89_ops import render_tiled`` raises ImportError;
-- activations and weights must be bfloat16 (the dtype the FlashVSR DiT runs
-  in); the reference's kernels also accept fp16/fp32, these raise TypeError;
+- the reference's ops take bf16, fp16 or fp32 inputs and so do these
+  (output in x's type; FP8Linear output bf16, a non-bf16 bias rounded to
+  bf16 for its epilogue); this build's fused extensions and the ``enable()``
+  block path take bf16, the dtype the FlashVSR DiT runs in;
 - ``build_csr(keep)`` returns ``sel`` of width NK (``maxk = NK``, entries
   past ``cnt`` unspecified) instead of trimming to the largest count, so no
   host synchronisation is needed.
