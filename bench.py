@@ -87,7 +87,7 @@ def block_costs():
 
 def run_stack(args, torch, fv):
     from flashvsr_sm89_ops.block import DiTStack
-    from flashvsr_sm89_ops.lcsa import build_csr
+    from flashvsr_sm89_ops.lcsa import block_index
     from flashvsr_sm89_ops.lcsa.masks import window_plus_random_mask
     from flashvsr_sm89_ops.rope import wan_freqs_cis
 
@@ -100,7 +100,7 @@ def run_stack(args, torch, fv):
     cs = torch.view_as_real(wan_freqs_cis(F, H, W, HD).reshape(L, HD // 2)).to(dev)
     keep = window_plus_random_mask(HEADS, 2, 6, 11, 7, 10, seed=7, device=dev)
     kept = int(keep.sum().item())
-    index = build_csr(keep)
+    index = block_index(keep)
     tmap = (F, H, W)     # the attention computes the (2, 8, 8) window order of this grid
     torch.cuda.synchronize()
 

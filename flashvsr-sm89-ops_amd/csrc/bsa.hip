@@ -443,6 +443,10 @@ void bsa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__
 }
 
 // One wavefront per (head, query block) row: ballot compaction of the kept ids.
+// One row of the block index per wave: the kept block ids ascending, then the
+// other ids ascending -- the order of the reference's stable descending
+// argsort of keep (lcsa/triton_lcsa.py:67-68) -- and the kept count.  The
+// first pass counts the kept ids, so the second can place both groups.
 __global__ __launch_bounds__(256) void block_index_kernel(const uint8_t* __restrict__ keep,
                                                           int64_t rows, int64_t NK,
                                                           int32_t* __restrict__ sel,
@@ -452,14 +456,21 @@ __global__ __launch_bounds__(256) void block_index_kernel(const uint8_t* __restr
   if (row >= rows) return;
   const uint8_t* kr = keep + row * NK;
   int32_t* sr = sel + row * NK;
-  int base = 0;
+  int kept = 0;
+  for (int64_t c0 = 0; c0 < NK; c0 += 64)
+    kept += __popcll(__ballot(c0 + lane < NK && kr[c0 + lane] != 0));
+  int base = 0, rest = kept;
   for (int64_t c0 = 0; c0 < NK; c0 += 64) {
-    const bool f = c0 + lane < NK && kr[c0 + lane] != 0;
-    const uint64_t bal = __ballot(f);
-    if (f) sr[base + __popcll(bal & ((1ull << lane) - 1ull))] = (int32_t)(c0 + lane);
-    base += __popcll(bal);
+    const bool in = c0 + lane < NK;
+    const bool f = in && kr[c0 + lane] != 0;
+    const uint64_t below = (1ull << lane) - 1ull;
+    const uint64_t bk = __ballot(f), bn = __ballot(in && !f);
+    if (f) sr[base + __popcll(bk & below)] = (int32_t)(c0 + lane);
+    if (in && !f) sr[rest + __popcll(bn & below)] = (int32_t)(c0 + lane);
+    base += __popcll(bk);
+    rest += __popcll(bn);
   }
-  if (lane == 0) cnt[row] = base;
+  if (lane == 0) cnt[row] = kept;
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }

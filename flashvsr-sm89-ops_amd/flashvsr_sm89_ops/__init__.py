@@ -16,9 +16,9 @@ What differs from the reference package at its public surface:
   (output in x's type; FP8Linear output bf16, a non-bf16 bias rounded to
   bf16 for its epilogue); this build's fused extensions and the ``enable()``
   block path take bf16, the dtype the FlashVSR DiT runs in;
-- ``build_csr(keep)`` returns ``sel`` of width NK (``maxk = NK``, entries
-  past ``cnt`` unspecified) instead of trimming to the largest count, so no
-  host synchronisation is needed.
+- ``build_csr(keep)`` returns the reference's triple (host read of the
+  largest count included); ``lcsa.block_index(keep)`` is the untrimmed form
+  (``maxk = NK``, no host read) that the attention paths use.
 """
 from .compat_bsa import active_backend, ensure_bsa_available
 

@@ -51,7 +51,7 @@ from .fused_adaln import (fused_gate_add, fused_gate_add_layer_norm,
                           fused_ln_modulate_quant, layer_norm)
 from .fused_rms_rope import fused_rms_rope, fused_rms_rope_qkv_rows
 from .lcsa.draft import draft_index
-from .lcsa.hip_lcsa import block_sparse_attention_strided, build_csr
+from .lcsa.hip_lcsa import block_index, block_sparse_attention_strided
 
 WINDOW = (2, 8, 8)              # frames x rows x columns of one attention window (128 tokens)
 _TOKENS_PER_WINDOW = WINDOW[0] * WINDOW[1] * WINDOW[2]
@@ -281,7 +281,7 @@ def _window_self_attention(dit, self, x, freqs, f, h, w, topk, kv_len, is_stream
         q_w = q2.index_select(0, tok.long()).view(-1, _TOKENS_PER_WINDOW, D)
         mask = dit.generate_draft_block_mask(B, self.num_heads, steps, q_w, k_w, topk=topk,
                                              local_attn_mask=local)
-        index = build_csr(mask[0] if mask.dim() == 4 else mask)
+        index = block_index(mask[0] if mask.dim() == 4 else mask)
     out = torch.empty((L, D), dtype=q.dtype, device=q.device)
     hd = self.head_dim
     block_sparse_attention_strided(

@@ -6,8 +6,10 @@ block mask ``[H, NQ, NK]``; rows with no kept block output 0.
 
 Differences in mechanism, not in results:
  - the block index is built on the device (``fvsr_block_index``, a ballot
-   compaction) with ``MAXK = NK``, so there is no host sync
-   (the reference's ``int(cnt.max())``, triton_lcsa.py:68);
+   compaction); ``build_csr`` returns the reference's triple (rows trimmed to
+   ``maxk = max(cnt.max(), 1)``, which reads ``cnt`` back to the host as the
+   reference does, triton_lcsa.py:68), while the attention entry points use
+   ``block_index``, the same rows untrimmed (``maxk = NK``) and no host read;
  - the attention kernel reads only kept key blocks, with MFMA bf16 QK^T and
    PV and an fp32 online softmax.
 
@@ -26,12 +28,11 @@ from .. import _lib
 BLOCK = 128
 
 
-def build_csr(keep: torch.Tensor):
-    """keep [H, NQ, NK] bool -> (sel [H, NQ, NK] int32, cnt [H, NQ] int32, NK).
-
-    Kept block ids come first in ascending order (triton_lcsa.py:64-71); the
-    entries after cnt are unspecified.  MAXK is NK, so nothing is read back to
-    the host."""
+def block_index(keep: torch.Tensor):
+    """keep [H, NQ, NK] bool -> (sel [H, NQ, NK] int32, cnt [H, NQ] int32, NK):
+    each row of sel holds the kept block ids ascending, then the others
+    ascending (the reference's stable descending argsort, triton_lcsa.py:67),
+    untrimmed, so nothing is read back to the host."""
     _lib.require_gpu(keep)
     H, NQ, NK = keep.shape
     # a bool mask is already one byte per entry: no conversion kernel
@@ -40,8 +41,18 @@ def build_csr(keep: torch.Tensor):
     sel = torch.empty((H, NQ, max(NK, 1)), dtype=torch.int32, device=keep.device)
     cnt = torch.empty((H, NQ), dtype=torch.int32, device=keep.device)
     _lib.check(_lib.lib().fvsr_block_index(k8.data_ptr(), H, NQ, NK, sel.data_ptr(),
-                                           cnt.data_ptr(), _lib.stream(keep)), "build_csr")
+                                           cnt.data_ptr(), _lib.stream(keep)), "block_index")
     return sel, cnt, max(NK, 1)
+
+
+def build_csr(keep: torch.Tensor):
+    """keep [H, NQ, NK] bool -> (sel [H, NQ, MAXK] int32, cnt [H, NQ] int32,
+    MAXK), the reference's build_csr (triton_lcsa.py:64-71): MAXK =
+    max(cnt.max(), 1), read back to the host, and sel the first MAXK entries
+    of each row of block_index's order."""
+    sel, cnt, _ = block_index(keep)
+    maxk = max(int(cnt.max()), 1)
+    return sel[..., :min(maxk, keep.shape[-1])].contiguous(), cnt, maxk
 
 
 def _check_extent(t, rows: int, tok_stride: int, head_stride: int, heads: int, head_dim: int,
@@ -90,8 +101,11 @@ def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, 
     if index is None:
         H, NQ, NK = keep.shape
     else:
+        # The index alone does not say how many key blocks k/v hold: raster
+        # k/v of the window grid hold NQ, otherwise the rows' width (NK for
+        # block_index, at most NK for build_csr's trimmed rows) is used.
         H, NQ = index[1].shape
-        NK = index[2]
+        NK = NQ if window is not None and window[3] else index[2]
     if window is not None:
         if q_map is not None or kv_map is not None:
             raise ValueError("give either token maps or a window grid, not both")
@@ -102,7 +116,7 @@ def block_sparse_attention_strided(q, k, v, keep, sm_scale=None, *, heads: int, 
         if kv_raster and NK != NQ:
             raise ValueError("raster-order k/v need as many key blocks as query blocks")
     _lib.require_gpu(q, k, v, out, q_map, kv_map)
-    sel, cnt, maxk = build_csr(keep) if index is None else index
+    sel, cnt, maxk = block_index(keep) if index is None else index
     if H != heads:
         raise ValueError(f"block mask has {H} heads, tensors have {heads}")
     _lib.require_gpu(sel, cnt)

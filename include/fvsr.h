@@ -280,8 +280,11 @@ int fvsr_rms_rope_qkv_rows(const void* q, const void* k, const void* v, const vo
 /*
  * Block index from a bool block mask, reference build_csr
  * (flashvsr_sm89_ops/lcsa/triton_lcsa.py:64-71) without its host sync:
- * keep uint8 [H, NQ, NK] -> sel int32 [H, NQ, NK] (kept block ids ascending,
- * the rest of each row unspecified) and cnt int32 [H, NQ].
+ * keep uint8 [H, NQ, NK] -> sel int32 [H, NQ, NK] and cnt int32 [H, NQ].
+ * Each row of sel holds the kept block ids ascending, then the other ids
+ * ascending: the reference's stable descending argsort of keep, before it
+ * trims the rows to maxk = max(cnt) (a host read this entry point leaves to
+ * the caller).
  */
 int fvsr_block_index(const uint8_t* keep, int64_t H, int64_t NQ, int64_t NK, int32_t* sel,
                      int32_t* cnt, void* stream);

@@ -520,15 +520,23 @@ def test_rms_rope_golden_complex128_freqs(ops):
 # ----------------------------------------------------------------------------- attention
 
 def test_block_index_vs_oracle(ops):
-    keep = O.random_block_mask(3, 40, 150, 0.3, seed=3)
-    keep[1, 5] = False  # an empty row
-    sel, cnt, maxk = ops.build_csr(torch.from_numpy(keep).to(DEV))
-    rs, rc, _ = O.build_csr(keep)
-    sel, cnt = sel.cpu().numpy(), cnt.cpu().numpy()
-    assert np.array_equal(cnt, rc) and maxk == 150
-    for h in range(3):
-        for i in range(40):
-            assert np.array_equal(sel[h, i, :cnt[h, i]], rs[h, i, :cnt[h, i]])
+    """build_csr returns the reference's triple exactly (lcsa/triton_lcsa.py:
+    64-71: rows trimmed to max(cnt, 1), kept ids then the others, ascending);
+    block_index the same rows untrimmed (maxk = NK)."""
+    from flashvsr_sm89_ops.lcsa import block_index
+    for seed, (H, NQ, NK, dens) in enumerate([(3, 40, 150, 0.3), (2, 9, 70, 0.05),
+                                             (1, 4, 5, 0.0)]):
+        keep = O.random_block_mask(H, NQ, NK, dens, seed=3 + seed)
+        keep[0, 1] = False  # an empty row
+        kd = torch.from_numpy(keep).to(DEV)
+        sel, cnt, maxk = ops.build_csr(kd)
+        rs, rc, rm = O.build_csr(keep)
+        assert maxk == rm and tuple(sel.shape) == rs.shape and sel.is_contiguous()
+        assert np.array_equal(sel.cpu().numpy(), rs) and np.array_equal(cnt.cpu().numpy(), rc)
+        fs, fc, fm = block_index(kd)
+        full = np.argsort(~keep, axis=-1, kind="stable").astype(np.int32)
+        assert fm == NK and np.array_equal(fs.cpu().numpy(), full)
+        assert np.array_equal(fc.cpu().numpy(), rc)
 
 
 def _draft_check(ops, qb, kb, H, q_temporal, local, topk, q_map=None, k_map=None, qw=None,

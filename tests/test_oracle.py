@@ -436,9 +436,25 @@ def test_build_csr_brute_force():
     for h in range(3):
         for i in range(5):
             ids = [j for j in range(7) if keep[h, i, j]]
+            rest = [j for j in range(7) if not keep[h, i, j]]
             assert cnt[h, i] == len(ids)
-            assert list(sel[h, i, :len(ids)]) == ids
+            assert list(sel[h, i]) == (ids + rest)[:maxk]
     assert maxk == cnt.max()
+
+
+def test_build_csr_vs_reference_torch_expression():
+    """The reference's own expressions (lcsa/triton_lcsa.py:66-69) run by
+    torch: cnt, maxk = max(cnt.max(), 1) and the stable descending argsort of
+    keep as int8, trimmed to maxk; an all-empty mask gives maxk 1."""
+    for seed, dens in enumerate((0.3, 0.02, 0.0)):
+        keep = O.random_block_mask(4, 11, 33, dens, seed=10 + seed)
+        t = torch.from_numpy(keep)
+        tc = t.sum(-1)
+        tm = max(int(tc.max()), 1)
+        ts = torch.argsort(t.to(torch.int8), dim=-1, descending=True, stable=True)[..., :tm]
+        sel, cnt, maxk = O.build_csr(keep)
+        assert maxk == tm and np.array_equal(cnt, tc.numpy())
+        assert np.array_equal(sel, ts.to(torch.int32).numpy())
 
 
 def test_c4_mask_density_and_diagonal():
