@@ -252,3 +252,71 @@ def test_rms_rope_fp32_holding_bf16_values_equals_bf16_path(ops, fhw):
         of = ops.fused_rms_rope(x.float(), w, f, rope=rope)
         assert of.dtype == torch.float32
         assert torch.equal(ob.float(), of)
+
+
+@pytest.mark.parametrize("dtype", F16_F32)
+def test_fp8_ffn_dtypes(ops, dtype):
+    """FP8FFN over fp16 / fp32 Linears (fp8_ffn.py:84-96), per tensor (the
+    reference's default): mm2 against the oracle's GEMM of the codes the
+    device fed it, and the whole chain (input codes in x's type, mm0, GELU
+    requantisation, mm2) against the oracle's at the chain bar (at most 0.1%
+    of elements beyond rtol/atol 2e-2)."""
+    from flashvsr_sm89_ops import FP8FFN, FP8Linear
+    g = torch.Generator().manual_seed(11)
+    D, F = 512, 1024
+
+    def lin(n, k):
+        m = torch.nn.Linear(k, n, dtype=dtype)
+        with torch.no_grad():
+            m.weight.copy_(torch.randn(n, k, generator=g) * 0.03)
+            m.bias.copy_(torch.randn(n, generator=g) * 0.1)
+        return m.to(DEV)
+    l0, l2 = lin(F, D), lin(D, F)
+    ffn = FP8FFN(FP8Linear(l0), FP8Linear(l2))
+    x = (torch.randn(2, 300, D, generator=g) * 2).to(dtype).to(DEV)
+    seen = []
+    for m in (ffn.lin2,):
+        real = m._mm
+        m._mm = lambda x8, s, out=None, real=real: (seen.append((codes(x8), host_f(s).reshape(-1))),
+                                                    real(x8, s, out=out))[1]
+    y = ffn(x)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 300, D) and y.dtype == torch.bfloat16
+    w0q, w0s = O.quantize_weight_values(host_f(l0.weight), DT[dtype])
+    w2q, w2s = O.quantize_weight_values(host_f(l2.weight), DT[dtype])
+    xq, xs = O.quantize_fp8_values(host_f(x).reshape(-1, D))
+    h_ref = O.fp8_gemm(xq, xs, w0q, w0s, O.bf16(host_f(l0.bias)))
+    h8, hs = seen[0]                      # the codes the device fed mm2
+    out = host_f(y).reshape(-1, D)
+    assert (np.abs(out - O.fp8_gemm(h8, hs, w2q, w2s, O.bf16(host_f(l2.bias))))
+            <= 2e-2 + 2e-2 * np.abs(out)).all()
+    ref = O.fp8_gemm(*O.quantize_fp8(O.bf16_bits(h_ref), per_row=False, gelu=True), w2q, w2s,
+                     O.bf16(host_f(l2.bias)))
+    bad = np.abs(out - ref) > 2e-2 + 2e-2 * np.abs(ref)
+    assert bad.mean() <= 1e-3, f"chain {bad.mean():.2e}"
+
+
+@pytest.mark.parametrize("dtype", F16_F32)
+def test_dtype_paths_edge_shapes(ops, dtype):
+    """Empty inputs, D not a multiple of 8 (RMSNorm without RoPE, LN,
+    gate_add) and an odd row count, against the oracle."""
+    q, s = ops.quantize_fp8(torch.zeros(0, 24, dtype=dtype, device=DEV))
+    assert q.shape == (0, 24) and s.shape == (1,) and float(s) == 0.0
+    q, s = ops.quantize_fp8(torch.zeros(0, 24, dtype=dtype, device=DEV), per_token=True)
+    assert q.shape == (0, 24) and s.shape == (0, 1)
+    x = rnd((1, 7, 100), 31, dtype)
+    w = (1 + 0.1 * rnd(100, 32, torch.float32)).to(dtype)
+    out = ops.fused_rms_rope(x.to(DEV), w.to(DEV), None, rope=False)
+    ref = O.rms_rope(x.float().numpy(), w.float().numpy(), rope=False)
+    close(host_f(out), as_type(ref, dtype))
+    sc, sh = rnd((1, 1, 100), 33, dtype, 0.1), rnd((1, 1, 100), 34, dtype, 0.1)
+    out = ops.fused_ln_modulate(x.to(DEV), sc.to(DEV), sh.to(DEV))
+    close(host_f(out), as_type(O.ln_modulate(x.float().numpy(), sc.float().numpy(),
+                                             sh.float().numpy()), dtype))
+    r = rnd((1, 7, 100), 35, dtype)
+    out = ops.fused_gate_add(x.to(DEV), sc.to(DEV), r.to(DEV))
+    assert np.array_equal(host_f(out), as_type(O.gate_add(x.float().numpy(), sc.float().numpy(),
+                                                          r.float().numpy()), dtype))
+    q, s = ops.quantize_fp8(x.reshape(7, 100).to(DEV), per_token=True)
+    rq, rs = O.quantize_fp8_values(x.reshape(7, 100).float().numpy(), per_row=True)
+    assert np.array_equal(codes(q), rq) and np.array_equal(host_f(s).reshape(-1), rs)
