@@ -442,7 +442,6 @@ void bsa_fwd_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__
   }
 }
 
-// One wavefront per (head, query block) row: ballot compaction of the kept ids.
 // One row of the block index per wave: the kept block ids ascending, then the
 // other ids ascending -- the order of the reference's stable descending
 // argsort of keep (lcsa/triton_lcsa.py:67-68) -- and the kept count.  The
