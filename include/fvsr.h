@@ -304,7 +304,8 @@ int64_t fvsr_draft_workspace_floats(int64_t H, int64_t D, int64_t NQ, int64_t NK
  * q, k: bf16, token j of block n at row map[n*128 + j] (row n*128 + j when the
  * map is NULL), rows q_tok_stride / k_tok_stride elements apart; H*D channels.
  * Outputs (either or both): keep uint8 [H, NQ, NK]; sel int32 [H, NQ, NK] and
- * cnt int32 [H, NQ] in fvsr_block_index's form (kept block ids ascending).
+ * cnt int32 [H, NQ]: the first cnt entries of each sel row are the kept block
+ * ids ascending, as in fvsr_block_index; the rest of the row is unspecified.
  * workspace: fvsr_draft_workspace_floats(H, D, NQ, NK).
  * Requires D % 8 == 0, token strides % 8 == 0, 16-byte aligned q and k, and
  * 2*D + NK <= 3968.
