@@ -67,8 +67,10 @@ int64_t fvsr_quant_workspace_floats(int64_t rows, int64_t cols, int mode);
  * elements), optionally of tanh-GELU(x) (gelu = 1).
  *   mode FVSR_SCALE_TENSOR: one scale, reference quantize_fp8
  *     (flashvsr_sm89_ops/fp8_quant.py:42-55) and fused_gelu_quant_fp8
- *     (fp8_ffn.py:57-72); scale_out[0] = amax/448.
- *   mode FVSR_SCALE_ROW: one scale per row, scale_out[rows].
+ *     (fp8_ffn.py:57-72); scale_out[0] = amax/448 as torch evaluates the
+ *     reference's `amax / FP8_MAX` on the GPU, amax * fl(1/448).  The codes
+ *     are those of x / (max(amax, 1e-12) / 448), true divisions.
+ *   mode FVSR_SCALE_ROW: one scale per row, scale_out[rows], the same way.
  * codes: uint8 [rows, cols] contiguous.  workspace: fvsr_quant_workspace_floats.
  */
 int fvsr_quant_fp8(const void* x, int64_t rows, int64_t cols, int64_t ld, int mode, int gelu,
